@@ -1,0 +1,298 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 paged KV-cache path on one MI355X.
+
+Default workload (the headline metric): flash-decoding paged
+attention, batch 64, ragged contexts L ~ U[128, 4096], GQA 14 query / 2 KV
+heads, head_dim 64, f16 KV in 16-token pages, block tables a seeded permutation
+of a 65,536-page pool, 512-token split-K partitions with a log-sum-exp merge.
+
+One step = one attention launch over the whole batch, inputs resident in HBM.
+Each step reads a different layer's pools (--layers, default 8 x 537 MB), so
+the >= 2 x 256 MB working set defeats the 256 MB Infinity Cache and the rate
+is HBM, not MALL. value = algorithmic bytes / time (GB/s):
+    per row  512*L (K+V, f16) + 3584 (q) + 3584 (out) + 4*ceil(L/16) (page ids) + 8
+The roofline fraction is against the nominal 8 TB/s. cpu_baseline times the
+reference's own CPU attention (oracle/_ref: src/ops.cpp + src/threadpool.cpp,
+-O3 -mavx2 -mfma) on the same batch, rows gathered to contiguous fp32 first
+(gather timed separately), on this host's cores.
+
+Other configs (--config 2|4|5) print the same JSON shape for DESIGN.md tables.
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+NH, NKV, HD, THETA, PAGE = 14, 2, 64, 1e6, 16
+QD, KVD = NH * HD, NKV * HD
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged decode-attn HBM GB/s (% of 8 TB/s) + attn tok/s at batch 64, 1 GPU"
+KV_CODES = {"f32": 0, "f16": 1, "bf16": 2}
+KV_BYTES = {"f32": 4, "f16": 2, "bf16": 2}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def decode_bytes(lens, kv_bytes: int) -> int:
+    """Algorithmic HBM bytes of one decode-attention launch."""
+    return int(sum(2 * KVD * kv_bytes * L + 2 * QD * 4 + 4 * math.ceil(L / PAGE) + 8 for L in lens))
+
+
+def make_tables(rng, lens, num_pages, max_pages):
+    perm = rng.permutation(num_pages).astype(np.int32)
+    tables = np.zeros((len(lens), max_pages), np.int32)
+    nxt = 0
+    for s, n in enumerate(lens):
+        k = (int(n) + PAGE - 1) // PAGE
+        tables[s, :k] = perm[nxt:nxt + k]
+        nxt += k
+    return tables
+
+
+def fill_pool(torch, n_rows, kv, gen, dev):
+    dt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[kv]
+    return torch.randn((n_rows, KVD), generator=gen, device=dev, dtype=dt)
+
+
+def time_steps(torch, step, steps, warmup, stream):
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        step(warmup + i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def cpu_baseline_decode(O, lens, k_host, v_host, tables, kv, q_host, budget_s=10.0):
+    """Reference CPU attention per row over a contiguous fp32 gather of its pages."""
+    use_ref = O.ref_available()
+    cores = min(O.physical_cores(), 16)
+    if use_ref:
+        O.ref().ref_set_num_threads(cores)
+    gather_s, attn_s, batches = [], [], 0
+    t_start = time.perf_counter()
+    while True:
+        g_tot = a_tot = 0.0
+        for r, L in enumerate(lens):
+            t0 = time.perf_counter()
+            idx = (tables[r, np.arange(L) // PAGE].astype(np.int64) * PAGE + np.arange(L) % PAGE)
+            kc = np.ascontiguousarray(k_host[idx], np.float32)
+            vc = np.ascontiguousarray(v_host[idx], np.float32)
+            t1 = time.perf_counter()
+            if use_ref:
+                O.ref_attention(q_host[r], kc, vc, L - 1, NH, NKV, HD)
+            else:
+                O.attention(q_host[r], kc, vc, L - 1, NH, NKV, HD, threads=cores)
+            t2 = time.perf_counter()
+            g_tot += t1 - t0
+            a_tot += t2 - t1
+        gather_s.append(g_tot)
+        attn_s.append(a_tot)
+        batches += 1
+        if time.perf_counter() - t_start >= budget_s:
+            break
+    t = float(np.median(attn_s))
+    return {
+        "value": round(decode_bytes(lens, KV_BYTES[kv]) / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "reference" if use_ref else "port",
+        "sample": (f"the full batch ({len(lens)} rows, same contexts), {batches} passes in "
+                   f"{time.perf_counter() - t_start:.1f} s; median attention time per batch "
+                   f"{t * 1e3:.1f} ms; per-row gather to contiguous fp32 (excluded) "
+                   f"{float(np.median(gather_s)) * 1e3:.1f} ms"),
+        "attn_tok_per_s": round(len(lens) / t, 1),
+    }
+
+
+def bench_decode(args, torch, ie, O):
+    dev = torch.device("cuda:0")
+    kv = args.kv or "f16"
+    rng = np.random.default_rng(args.seed)
+    B, num_pages = 64, 65536
+    lens = rng.integers(128, 4097, B)
+    max_pages = 4096 // PAGE
+    tables = make_tables(rng, lens, num_pages, max_pages)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    log(f"config 3: seed {args.seed}, {args.layers} layers x 2 x {num_pages} pages of {kv}")
+    k_pools = [fill_pool(torch, num_pages * PAGE, kv, gen, dev) for _ in range(args.layers)]
+    v_pools = [fill_pool(torch, num_pages * PAGE, kv, gen, dev) for _ in range(args.layers)]
+    q = torch.randn((B, QD), generator=gen, device=dev, dtype=torch.float32)
+    out = torch.empty((B, QD), device=dev, dtype=torch.float32)
+    d_tab = torch.from_numpy(tables).to(dev)
+    d_pos = torch.from_numpy((lens - 1).astype(np.int32)).to(dev)
+    d_seq = torch.arange(B, dtype=torch.int32, device=dev)
+    ct = args.chunk_tokens or 512
+    nc = ie.attention_chunks(4096, ct)
+    ws = ie.attention_workspace(B, NH, HD, nc)
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        l = i % args.layers
+        ie.attention(out, q, k_pools[l], v_pools[l], d_pos, d_seq, d_tab, max_pages, nc, ct, ws,
+                     NH, NKV, HD)
+
+    ms = time_steps(torch, step, args.steps, args.warmup, stream)
+    nbytes = decode_bytes(lens, KV_BYTES[kv])
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res = {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "config 3: flash-decoding paged attention, batch 64, "
+                               "L~U[128,4096], GQA 14q/2kv, head_dim 64, 16-token pages, "
+                               "65,536-page pools, 512-token split-K + LSE merge",
+                   "kv_dtype": kv, "batch": B, "chunk_tokens": ct, "num_chunks": nc,
+                   "layers_rotated": args.layers, "seed": args.seed,
+                   "context_tokens": int(lens.sum())},
+        "attn_tok_per_s": round(B / (ms * 1e-3), 1),
+        "context_tok_per_s": round(float(lens.sum()) / (ms * 1e-3), 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("decode")},
+        "algorithmic_bytes_per_step": nbytes,
+    }
+    if not args.no_cpu:
+        kh = O.widen_kv(k_pools[0].cpu().view(torch.int16).numpy().view(np.uint16), KV_CODES[kv]) \
+            if kv != "f32" else k_pools[0].cpu().numpy()
+        vh = O.widen_kv(v_pools[0].cpu().view(torch.int16).numpy().view(np.uint16), KV_CODES[kv]) \
+            if kv != "f32" else v_pools[0].cpu().numpy()
+        res["cpu_baseline"] = cpu_baseline_decode(O, [int(x) for x in lens], kh, vh, tables, kv,
+                                                  q.cpu().numpy(), args.cpu_seconds)
+    return res
+
+
+def bench_append(args, torch, ie, O):
+    """Config 2: fused RoPE + paged append, 64 rows; plus a rows-per-launch sweep."""
+    dev = torch.device("cuda:0")
+    kv = args.kv or "f16"
+    rng = np.random.default_rng(args.seed)
+    num_pages, max_pos = 65536, 4096
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    k_pool = fill_pool(torch, num_pages * PAGE, kv, gen, dev)
+    v_pool = fill_pool(torch, num_pages * PAGE, kv, gen, dev)
+    table = ie.rope_table(max_pos, HD, THETA).to(dev)
+    stream = torch.cuda.current_stream()
+    sweep = []
+    for rows in ([64] + ([256, 1024, 4096, 16384, 65536, 131072] if args.sweep else [])):
+        seqs = max(1, rows // 64)
+        max_pages = num_pages // seqs
+        tables = rng.permutation(num_pages)[:seqs * max_pages].astype(np.int32).reshape(seqs, -1)
+        pos = rng.integers(1, min(max_pos, max_pages * PAGE), rows).astype(np.int32)
+        d_tab = torch.from_numpy(tables).to(dev)
+        d_pos = torch.from_numpy(pos).to(dev)
+        d_seq = torch.from_numpy((np.arange(rows) % seqs).astype(np.int32)).to(dev)
+        q = torch.randn((rows, QD), generator=gen, device=dev)
+        k = torch.randn((rows, KVD), generator=gen, device=dev)
+        v = torch.randn((rows, KVD), generator=gen, device=dev)
+        for with_q in (False, True):
+            def step(i):
+                ie.rope_and_cache(q if with_q else None, k, v, k_pool, v_pool, table, d_pos, d_seq,
+                                  d_tab, max_pages, NH, NKV, HD)
+            ms = time_steps(torch, step, args.steps, args.warmup, stream)
+            per_row = (1024 + 2 * KVD * KV_BYTES[kv] + 8 + 4) + (2 * QD * 4 if with_q else 0)
+            sweep.append({"rows": rows, "with_q": with_q, "us_per_launch": round(ms * 1e3, 3),
+                          "gbs": round(rows * per_row / (ms * 1e-3) / 1e9, 2)})
+    head = [s for s in sweep if s["rows"] == 64 and not s["with_q"]][0]
+    return {
+        "metric": "paged RoPE+KV append GB/s at batch 64 (K/V only), 1 GPU",
+        "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(head["us_per_launch"] / 1e3, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "config 2: RoPE + paged KV append, 64 rows, pos~U[1,4096), "
+                               "65,536-page pool", "kv_dtype": kv, "seed": args.seed},
+        "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 5),
+                     "traffic": traffic_from_profiles("append")},
+        "sweep": sweep,
+    }
+
+
+def traffic_from_profiles(kernel: str):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE runs, as committed
+    under profiles/ (null when that measurement has not been made)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(kernel)
+
+
+def copy_probe(torch, n_bytes=2 << 30):
+    """Device-to-device copy bandwidth (read + write), the measured HBM ceiling."""
+    a = torch.empty(n_bytes // 4, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(10):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / 10
+    del a, b
+    return round(2 * n_bytes / (ms * 1e-3) / 1e9, 1)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3])
+    ap.add_argument("--kv", choices=list(KV_CODES), default=None)
+    ap.add_argument("--chunk-tokens", type=int, default=None)
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--seed", type=int, default=20263)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--sweep", action="store_true", help="config 2: rows-per-launch sweep")
+    ap.add_argument("--probe", action="store_true", help="also measure device copy bandwidth")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this path has no multi-GPU mode (the paged KV "
+              "cache would shard by sequence, one pool per GPU, with no exchange); run with "
+              "--gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__ as g
+    import oracle as O
+
+    ie = g.load()
+    ie.lib()
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    res = bench_decode(args, torch, ie, O) if args.config == 3 else bench_append(args, torch, ie, O)
+    if args.probe:
+        res["measured_copy_gbs"] = copy_probe(torch)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,199 @@
+/* ie_hip.h -- C ABI of the MI355X (gfx950) paged KV-cache path.
+ *
+ * Host code calls these entry points with device pointers, as the reference
+ * engine calls its CUDA kernel launchers (src/cuda/kernels.cuh:69-102). Every
+ * entry point queues its kernels on `stream` and returns at once; results are
+ * ready after the stream is synchronised. Every function returns 0 on success
+ * or a nonzero IE_HIP_E* code; ie_hip_last_error() then gives the message for
+ * the calling thread. No exception crosses this boundary.
+ *
+ * Paged KV cache (reference: src/cuda/kernels.cuh:14-38). Each layer has a
+ * K pool and a V pool of `num_pages` pages; a page holds 16 token rows of
+ * kv_dim = n_kv_heads * head_dim elements, row-major:
+ *     pool[(page * 16 + pos % 16) * kv_dim + kv_head * head_dim + d]
+ * Position `pos` of sequence `seq` lives in page
+ *     tables[seq * max_pages + pos / 16].
+ * Elements are float32, IEEE binary16 or bfloat16 (kv_dtype); all arithmetic
+ * is float32 (MFMA tiles accumulate in float32).
+ */
+#ifndef IE_HIP_H_
+#define IE_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IE_HIP_PAGE_SIZE 16
+
+/* KV element types. The reference has f32 and f16 (KvLayout::f16,
+ * src/cuda/kernels.cuh:37); bf16 is added here. */
+enum { IE_KV_F32 = 0, IE_KV_F16 = 1, IE_KV_BF16 = 2 };
+
+/* Status codes. */
+enum {
+  IE_HIP_OK = 0,
+  IE_HIP_EINVAL = 1,   /* bad argument or unsupported shape */
+  IE_HIP_ELAUNCH = 2,  /* a HIP call or kernel launch failed */
+  IE_HIP_EFULL = 3,    /* page pool exhausted ("KV cache full: no free pages") */
+  IE_HIP_ERANGE = 4,   /* sequence longer than the maximum */
+  IE_HIP_ESEQ = 5      /* invalid or closed sequence id */
+};
+
+/* Where each sequence's KV rows live. Passed by value, like the reference's
+ * KvLayout (src/cuda/kernels.cuh:33-38), plus `num_pages`, the pool size: the
+ * kernels skip (never dereference) page ids outside [0, num_pages). */
+typedef struct ie_kv_layout {
+  const int32_t* tables; /* device [num_sequences * max_pages] page ids */
+  int32_t max_pages;     /* row stride of `tables` */
+  int32_t page_size;     /* must be IE_HIP_PAGE_SIZE */
+  int32_t kv_dtype;      /* IE_KV_F32 | IE_KV_F16 | IE_KV_BF16 */
+  int32_t num_pages;     /* pages in each pool */
+} ie_kv_layout;
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* ie_hip_last_error(void);
+
+/* Library version string and the device it was built for ("gfx950"). */
+const char* ie_hip_version(void);
+
+/* ---------------------------------------------------------------- RoPE ---
+ * Host-side RoPE table, computed with the host C library exactly as the
+ * reference's CPU rope does (src/ops.cpp:37-48): for p < n_pos, i < head_dim/2,
+ *   inv_freq[i]                    = 1 / powf(theta, float(2i) / float(head_dim))
+ *   table[p*head_dim + i]          = cosf(float(p) * inv_freq[i])
+ *   table[p*head_dim + head_dim/2 + i] = sinf(float(p) * inv_freq[i])
+ * `table` is host memory of n_pos * head_dim floats; upload it once. Replaces
+ * the device inv_freq + cosf/sinf of the reference (src/cuda/cuda_runner.cu:184-189,
+ * src/cuda/kernels.cu:290-291), which cannot match the CPU bit for bit. */
+int ie_hip_rope_table(float* table, int n_pos, int head_dim, float theta);
+
+/* Fused RoPE + paged KV append. Replaces rope_and_cache
+ * (src/cuda/kernels.cuh:69-74, kernels.cu:278-307,1334-1348).
+ * For each row t < T at position row_pos[t] of sequence row_seq[t]:
+ *   q[t] (if q != NULL) is rotated in place;
+ *   k[t] is rotated and stored (rounded to kv_dtype) at (row_seq[t], row_pos[t]);
+ *   v[t] is stored (rounded) at the same slot.
+ * The rotation is x0' = fma(x0, c, -(x1*s)), x1' = fma(x1, c, x0*s) with c, s
+ * read from `rope_table` ([table_positions, head_dim] from ie_hip_rope_table,
+ * device memory): bit-identical to the reference CPU rope. Rows whose position
+ * is outside [0, table_positions) or whose page is outside the pool are skipped.
+ *   q: [T, n_heads*head_dim] f32 (may be NULL)   k, v: [T, n_kv_heads*head_dim] f32
+ * head_dim must be 64 or 128. */
+int ie_hip_rope_and_cache(float* q, const float* k, const float* v, void* k_pool, void* v_pool,
+                          const float* rope_table, int table_positions, int T,
+                          const int32_t* row_pos, const int32_t* row_seq, ie_kv_layout kv,
+                          int n_heads, int n_kv_heads, int head_dim, hipStream_t stream);
+
+/* ---------------------------------------------------- decode attention ---
+ * Flash-decoding over pages. Replaces attention + attention_chunks
+ * (src/cuda/kernels.cuh:76-99, kernels.cu:338-507,1387-1420).
+ * Row t attends causally to positions 0..row_pos[t] of its sequence. Positions
+ * are cut into partitions ("chunks") of `chunk_tokens` (a multiple of 16); each
+ * (row, chunk) is one workgroup producing a partial softmax result, merged
+ * exactly by log-sum-exp. `num_chunks` must cover the longest context the
+ * launch may see (chunks past a row's position do nothing), so one launch
+ * shape serves every position, as a recorded graph needs.
+ *   q, out: [T, n_heads*head_dim] f32. GQA: head h reads kv head h / (n_heads/n_kv_heads).
+ * Supported: head_dim 64, n_heads/n_kv_heads <= 8 (the reference's limits at
+ * this head_dim), page size 16. */
+
+/* Chunk size (tokens, a multiple of 16) that gives T rows of up to
+ * `max_context` tokens enough workgroups to fill the device's compute units. */
+int ie_hip_attention_chunk_tokens(int T, int max_context);
+
+/* Chunks needed to cover `context_tokens` positions: ceil(context/chunk). */
+int ie_hip_attention_chunks(int context_tokens, int chunk_tokens);
+
+/* Bytes of workspace ie_hip_attention needs for T rows and num_chunks chunks
+ * (the reference's part_o + part_ml scratch, src/cuda/kernels.cuh:82-83, plus
+ * one counter per row). Allocate it once and zero-fill it once; every call
+ * leaves it ready for the next. Calls that overlap on one workspace race. */
+size_t ie_hip_attention_workspace_bytes(int T, int n_heads, int head_dim, int num_chunks);
+
+int ie_hip_attention(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                     const int32_t* row_pos, const int32_t* row_seq, ie_kv_layout kv,
+                     int num_chunks, int chunk_tokens, void* workspace, int n_heads,
+                     int n_kv_heads, int head_dim, hipStream_t stream);
+
+/* --------------------------------------------------- prefill attention ---
+ * Attention for T rows that are consecutive positions of ONE sequence
+ * (row_pos[t] = row_pos[0] + t), e.g. a prompt chunk already appended with
+ * ie_hip_rope_and_cache. Replaces attention_prefill_supported /
+ * attention_prefill (src/cuda/kernels.cuh:89-96, kernels.cu:527-776,1350-1385).
+ * f16/bf16 KV: QK^T and PV tiles on bf16 MFMA (split hi+lo operands, float32
+ * accumulation). f32 KV: float32 VALU tiles. No workspace. */
+int ie_hip_attention_prefill_supported(int n_heads, int n_kv_heads, int head_dim);
+int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, const void* v_pool,
+                             int T, const int32_t* row_pos, const int32_t* row_seq,
+                             ie_kv_layout kv, int n_heads, int n_kv_heads, int head_dim,
+                             hipStream_t stream);
+
+/* ------------------------------------------------------------- gathers ---
+ * dst[r, :] = src[rows[r], :] for r < R. Replaces gather_rows
+ * (src/cuda/kernels.cuh:101-102, kernels.cu:778-783,1422-1425). */
+int ie_hip_gather_rows(float* dst, const float* src, const int32_t* rows, int R, int dim,
+                       hipStream_t stream);
+
+/* Block-table gather of one sequence: dst[p, :] = pool row of (seq, p) for
+ * p < len, widened to float32 ([len, kv_dim]). The paged-to-contiguous copy the
+ * reference's self-test makes on the host (src/cuda/cuda_runner.cu:959-964),
+ * done on the device. */
+int ie_hip_gather_kv(float* dst, const void* pool, ie_kv_layout kv, int seq, int len, int kv_dim,
+                     hipStream_t stream);
+
+/* ------------------------------------------------------- page allocator ---
+ * The page pool / free list / page tables behind BatchRunner (reference:
+ * CudaEngine ctor src/cuda/cuda_runner.cu:191-204, open/close_sequence
+ * :240-252, ensure_pages :300-313, Sequence :133-137, make_batch_runner
+ * :612-622). Host-only bookkeeping; not thread-safe (one engine thread owns it,
+ * src/server.h:9-17). Pages are handed out LIFO from a free list initialised so
+ * that page 0 goes first; closing a sequence pushes its pages back in order. */
+typedef struct ie_page_pool ie_page_pool;
+
+/* Pool of num_pages pages for up to max_batch sequences of max_seq_len tokens.
+ * Returns NULL on bad arguments (see ie_hip_last_error). */
+ie_page_pool* ie_pages_create(int num_pages, int max_batch, int max_seq_len);
+void ie_pages_destroy(ie_page_pool* pool);
+
+/* Lowest free sequence slot, opened empty; -1 if all slots are busy. */
+int ie_pages_open_sequence(ie_page_pool* pool);
+/* Frees the sequence's pages. IE_HIP_ESEQ if seq is not open. */
+int ie_pages_close_sequence(ie_page_pool* pool, int seq);
+/* Makes positions 0..len-1 of seq backed by pages, taking pages from the free
+ * list (IE_HIP_EFULL when it runs out, IE_HIP_ERANGE past max_seq_len,
+ * IE_HIP_ESEQ for a closed id). Pages taken before a failure stay with seq. */
+int ie_pages_ensure(ie_page_pool* pool, int seq, int len);
+/* Tokens cached for seq (advanced by the caller after a step); -1 if closed. */
+int ie_pages_sequence_length(const ie_page_pool* pool, int seq);
+int ie_pages_set_sequence_length(ie_page_pool* pool, int seq, int len);
+/* Pages currently owned by seq, copied to out (at most cap); returns the count. */
+int ie_pages_sequence_pages(const ie_page_pool* pool, int seq, int32_t* out, int cap);
+int ie_pages_total_pages(const ie_page_pool* pool);
+int ie_pages_free_pages(const ie_page_pool* pool);
+int ie_pages_max_batch(const ie_page_pool* pool);
+int ie_pages_max_seq_len(const ie_page_pool* pool);
+int ie_pages_max_pages_per_seq(const ie_page_pool* pool);
+/* The host page table [max_batch * max_pages_per_seq]. It starts zero-filled;
+ * as in the reference, closing a sequence does not clear its old entries. */
+const int32_t* ie_pages_host_tables(const ie_page_pool* pool);
+/* Copies the host table to `device_tables` on `stream` if it changed since the
+ * last upload (the reference's dirty flag, src/cuda/cuda_runner.cu:379-383).
+ * *uploaded (if not NULL) is set to 1 when a copy was queued. The host table is
+ * staged through pinned memory owned by the pool. */
+int ie_pages_upload_tables(ie_page_pool* pool, int32_t* device_tables, hipStream_t stream,
+                           int* uploaded);
+
+/* Pages a sequence of `tokens` tokens needs: ceil(tokens / 16)
+ * (src/cuda/cuda_runner.cu:583). */
+int ie_pages_for(int tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IE_HIP_H_ */

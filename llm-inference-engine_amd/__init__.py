@@ -1,0 +1,283 @@
+"""Host-side Python mirror of the gfx950 paged KV-cache library (libie_hip.so).
+
+The library's C ABI is declared in include/ie_hip.h; this module binds it with
+ctypes and offers the reference's kernel-launcher interface
+(src/cuda/kernels.cuh:69-102) over torch tensors, plus the page allocator
+(src/cuda/cuda_runner.cu:191-313) as a class. torch supplies device memory
+and streams only; all compute happens in the HIP kernels. Nothing here falls
+back to a CPU implementation: every entry point raises if libie_hip.so is
+missing or a call fails.
+
+The package directory name is not an identifier; load it with ``load()`` from
+``__graft_entry__`` or import it through importlib (tests do).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libie_hip.so")
+PAGE_SIZE = 16
+KV_F32, KV_F16, KV_BF16 = 0, 1, 2
+KV_NAMES = {"f32": KV_F32, "f16": KV_F16, "bf16": KV_BF16}
+
+# Status codes (include/ie_hip.h).
+OK, EINVAL, ELAUNCH, EFULL, ERANGE, ESEQ = 0, 1, 2, 3, 4, 5
+
+
+class IeHipError(RuntimeError):
+    """A libie_hip call returned a nonzero status."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class KvLayout(ctypes.Structure):
+    """ie_kv_layout: the reference's KvLayout (src/cuda/kernels.cuh:33-38) + pool size."""
+
+    _fields_ = [("tables", ctypes.c_void_p), ("max_pages", ctypes.c_int32),
+                ("page_size", ctypes.c_int32), ("kv_dtype", ctypes.c_int32),
+                ("num_pages", ctypes.c_int32)]
+
+
+_vp, _i, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+_SIGS = {
+    "ie_hip_last_error": (ctypes.c_char_p, []),
+    "ie_hip_version": (ctypes.c_char_p, []),
+    "ie_hip_rope_table": (_i, [_vp, _i, _i, _f]),
+    "ie_hip_rope_and_cache": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, KvLayout, _i, _i,
+                                   _i, _vp]),
+    "ie_hip_attention_chunk_tokens": (_i, [_i, _i]),
+    "ie_hip_attention_chunks": (_i, [_i, _i]),
+    "ie_hip_attention_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i]),
+    "ie_hip_attention": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _vp, _i, _i, _i,
+                              _vp]),
+    "ie_hip_attention_prefill_supported": (_i, [_i, _i, _i]),
+    "ie_hip_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _i, _vp]),
+    "ie_hip_gather_rows": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "ie_hip_gather_kv": (_i, [_vp, _vp, KvLayout, _i, _i, _i, _vp]),
+    "ie_pages_create": (_vp, [_i, _i, _i]),
+    "ie_pages_destroy": (None, [_vp]),
+    "ie_pages_open_sequence": (_i, [_vp]),
+    "ie_pages_close_sequence": (_i, [_vp, _i]),
+    "ie_pages_ensure": (_i, [_vp, _i, _i]),
+    "ie_pages_sequence_length": (_i, [_vp, _i]),
+    "ie_pages_set_sequence_length": (_i, [_vp, _i, _i]),
+    "ie_pages_sequence_pages": (_i, [_vp, _i, _vp, _i]),
+    "ie_pages_total_pages": (_i, [_vp]),
+    "ie_pages_free_pages": (_i, [_vp]),
+    "ie_pages_max_batch": (_i, [_vp]),
+    "ie_pages_max_seq_len": (_i, [_vp]),
+    "ie_pages_max_pages_per_seq": (_i, [_vp]),
+    "ie_pages_host_tables": (_vp, [_vp]),
+    "ie_pages_upload_tables": (_i, [_vp, _vp, _vp, _vp]),
+    "ie_pages_for": (_i, [_i]),
+}
+EXPORTED = tuple(_SIGS)
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded libie_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                "(there is no fallback implementation)")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def last_error() -> str:
+    return lib().ie_hip_last_error().decode()
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        raise IeHipError(rc, last_error())
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _dtype_code(t) -> int:
+    import torch
+    return {torch.float32: KV_F32, torch.float16: KV_F16, torch.bfloat16: KV_BF16}[t.dtype]
+
+
+def layout(tables, max_pages: int, num_pages: int, kv_dtype: int) -> KvLayout:
+    return KvLayout(tables.data_ptr(), max_pages, PAGE_SIZE, kv_dtype, num_pages)
+
+
+def torch_kv_dtype(kv_dtype: int):
+    import torch
+    return {KV_F32: torch.float32, KV_F16: torch.float16, KV_BF16: torch.bfloat16}[kv_dtype]
+
+
+# ------------------------------------------------------------ kernels ----
+def rope_table(n_pos: int, head_dim: int, theta: float):
+    """Host RoPE table [n_pos, head_dim] (cos | sin) as a CPU float32 tensor."""
+    import torch
+    t = torch.empty((n_pos, head_dim), dtype=torch.float32)
+    _check(lib().ie_hip_rope_table(t.data_ptr(), n_pos, head_dim, theta))
+    return t
+
+
+def rope_and_cache(q, k, v, k_pool, v_pool, table, row_pos, row_seq, tables, max_pages: int,
+                   n_heads: int, n_kv_heads: int, head_dim: int, stream=None) -> None:
+    """rope_and_cache (src/cuda/kernels.cuh:72-74); q may be None (append only)."""
+    T = row_pos.numel()
+    kv = layout(tables, max_pages, k_pool.numel() // (PAGE_SIZE * n_kv_heads * head_dim),
+                _dtype_code(k_pool))
+    _check(lib().ie_hip_rope_and_cache(_ptr(q), _ptr(k), _ptr(v), _ptr(k_pool), _ptr(v_pool),
+                                       _ptr(table), table.shape[0], T, _ptr(row_pos),
+                                       _ptr(row_seq), kv, n_heads, n_kv_heads, head_dim,
+                                       _stream(stream)))
+
+
+def attention_chunk_tokens(T: int, max_context: int) -> int:
+    return int(lib().ie_hip_attention_chunk_tokens(T, max_context))
+
+
+def attention_chunks(context: int, chunk_tokens: int) -> int:
+    return int(lib().ie_hip_attention_chunks(context, chunk_tokens))
+
+
+def attention_workspace(T: int, n_heads: int, head_dim: int, num_chunks: int, device="cuda"):
+    import torch
+    n = int(lib().ie_hip_attention_workspace_bytes(T, n_heads, head_dim, num_chunks))
+    return torch.zeros(max(n, 256), dtype=torch.uint8, device=device)
+
+
+def attention(out, q, k_pool, v_pool, row_pos, row_seq, tables, max_pages: int, num_chunks: int,
+              chunk_tokens: int, workspace, n_heads: int, n_kv_heads: int, head_dim: int,
+              stream=None) -> None:
+    """Flash-decoding attention (src/cuda/kernels.cuh:84-87)."""
+    T = row_pos.numel()
+    kv = layout(tables, max_pages, k_pool.numel() // (PAGE_SIZE * n_kv_heads * head_dim),
+                _dtype_code(k_pool))
+    _check(lib().ie_hip_attention(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), T, _ptr(row_pos),
+                                  _ptr(row_seq), kv, num_chunks, chunk_tokens, _ptr(workspace),
+                                  n_heads, n_kv_heads, head_dim, _stream(stream)))
+
+
+def attention_prefill_supported(n_heads: int, n_kv_heads: int, head_dim: int) -> bool:
+    return bool(lib().ie_hip_attention_prefill_supported(n_heads, n_kv_heads, head_dim))
+
+
+def attention_prefill(out, q, k_pool, v_pool, row_pos, row_seq, tables, max_pages: int,
+                      n_heads: int, n_kv_heads: int, head_dim: int, stream=None) -> None:
+    """Prompt attention (src/cuda/kernels.cuh:93-96)."""
+    T = row_pos.numel()
+    kv = layout(tables, max_pages, k_pool.numel() // (PAGE_SIZE * n_kv_heads * head_dim),
+                _dtype_code(k_pool))
+    _check(lib().ie_hip_attention_prefill(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), T,
+                                          _ptr(row_pos), _ptr(row_seq), kv, n_heads, n_kv_heads,
+                                          head_dim, _stream(stream)))
+
+
+def gather_rows(dst, src, rows, stream=None) -> None:
+    """dst[r] = src[rows[r]] (src/cuda/kernels.cuh:101-102)."""
+    _check(lib().ie_hip_gather_rows(_ptr(dst), _ptr(src), _ptr(rows), rows.numel(), src.shape[-1],
+                                    _stream(stream)))
+
+
+def gather_kv(dst, pool, tables, max_pages: int, seq: int, length: int, kv_dim: int,
+              stream=None) -> None:
+    """Contiguous fp32 copy of one sequence's paged rows."""
+    kv = layout(tables, max_pages, pool.numel() // (PAGE_SIZE * kv_dim), _dtype_code(pool))
+    _check(lib().ie_hip_gather_kv(_ptr(dst), _ptr(pool), kv, seq, length, kv_dim, _stream(stream)))
+
+
+# -------------------------------------------------------- page allocator ----
+class PagePool:
+    """The BatchRunner page allocator (src/cuda/cuda_runner.cu:191-313), host side."""
+
+    def __init__(self, num_pages: int, max_batch: int, max_seq_len: int):
+        self._h = lib().ie_pages_create(num_pages, max_batch, max_seq_len)
+        if not self._h:
+            raise IeHipError(EINVAL, last_error())
+
+    def close(self) -> None:
+        if self._h:
+            lib().ie_pages_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def open_sequence(self) -> int:
+        return int(lib().ie_pages_open_sequence(self._h))
+
+    def close_sequence(self, seq: int) -> None:
+        _check(lib().ie_pages_close_sequence(self._h, seq))
+
+    def ensure(self, seq: int, length: int) -> None:
+        _check(lib().ie_pages_ensure(self._h, seq, length))
+
+    def sequence_length(self, seq: int) -> int:
+        return int(lib().ie_pages_sequence_length(self._h, seq))
+
+    def set_sequence_length(self, seq: int, length: int) -> None:
+        _check(lib().ie_pages_set_sequence_length(self._h, seq, length))
+
+    def pages(self, seq: int) -> list[int]:
+        n = lib().ie_pages_sequence_pages(self._h, seq, None, 0)
+        buf = (ctypes.c_int32 * max(n, 1))()
+        lib().ie_pages_sequence_pages(self._h, seq, buf, n)
+        return list(buf[:n])
+
+    @property
+    def total_pages(self) -> int:
+        return int(lib().ie_pages_total_pages(self._h))
+
+    @property
+    def free_pages(self) -> int:
+        return int(lib().ie_pages_free_pages(self._h))
+
+    @property
+    def max_batch(self) -> int:
+        return int(lib().ie_pages_max_batch(self._h))
+
+    @property
+    def max_seq_len(self) -> int:
+        return int(lib().ie_pages_max_seq_len(self._h))
+
+    @property
+    def max_pages_per_seq(self) -> int:
+        return int(lib().ie_pages_max_pages_per_seq(self._h))
+
+    def host_tables(self) -> list[int]:
+        n = self.max_batch * self.max_pages_per_seq
+        p = lib().ie_pages_host_tables(self._h)
+        return list((ctypes.c_int32 * n).from_address(p))
+
+    def upload_tables(self, device_tables, stream=None) -> bool:
+        up = ctypes.c_int(0)
+        _check(lib().ie_pages_upload_tables(self._h, device_tables.data_ptr(), _stream(stream),
+                                            ctypes.byref(up)))
+        return bool(up.value)
+
+
+def pages_for(tokens: int) -> int:
+    return int(lib().ie_pages_for(tokens))

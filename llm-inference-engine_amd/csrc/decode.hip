@@ -1,0 +1,379 @@
+// Flash-decoding attention over block-tabled KV pages (gfx950, wave64).
+//
+// Reference semantics: each row's causal GQA attention over its cached
+// positions, src/ops.cpp:70-108; the reference GPU path splits positions into
+// chunks and merges by log-sum-exp (src/cuda/kernels.cu:309-507).
+//
+// This file: the VALU partial kernel (all KV dtypes) and the merge.
+//   grid (T, n_kv_heads, num_chunks): rows vary fastest, so the dispatcher
+//   hands out chunk 0 of every row first and the empty tail chunks of short
+//   rows last; one 256-thread workgroup (4 waves) per (row, kv head, chunk).
+//   1. page ids of the chunk -> LDS; the group's queries -> LDS.
+//   2. scores: one lane per position, the position's key row read with 16-byte
+//      loads, dot products against the LDS queries (broadcast reads) for all
+//      query heads of the group; scores -> LDS.
+//   3. chunk max and sum of exp per head: wave64 butterfly reductions, then
+//      across the 4 waves through LDS.
+//   4. values: lanes = 8 positions x 8 dim-slices of 8 (16-byte loads), every
+//      value row read once for all heads of the group; butterfly-reduced over
+//      the 8 positions, then across waves through LDS.
+//   A row whose context fits one chunk writes `out` directly; otherwise the
+//   chunk writes (o, m, l) and decode_merge_kernel combines them:
+//   M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L.
+#include <algorithm>
+
+#include "common.hpp"
+#include "decode.hpp"
+
+namespace iehip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxChunk = 1024;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int KV, int HD, int G>
+__global__ void __launch_bounds__(kThreads)
+decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
+                    float* __restrict__ part_ml, const float* __restrict__ q,
+                    const typename Kv<KV>::elem* __restrict__ k_pool,
+                    const typename Kv<KV>::elem* __restrict__ v_pool,
+                    const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
+                    const int32_t* __restrict__ tables, int max_pages, int num_pages, int n_heads,
+                    int n_kv_heads, int num_chunks, int chunk_tokens, float scale) {
+  using K = Kv<KV>;
+  static_assert(HD == 64, "lanes 0..7 of a position group cover 64 dims in 8-element slices");
+  extern __shared__ float scores[];  // [G][chunk_tokens]
+  __shared__ __align__(16) float q_s[G][HD];
+  __shared__ int pages_s[kMaxChunk / IE_HIP_PAGE_SIZE];
+  __shared__ float red[kWaves][G];
+  __shared__ float red_o[kWaves][G][HD];
+  __shared__ float stat[2][G];
+
+  const int t = blockIdx.x, kvh = blockIdx.y, c = blockIdx.z;
+  const int p = row_pos[t];
+  const int s0 = c * chunk_tokens;
+  if (p < 0 || s0 > p) return;  // chunk in the future: nothing to do (uniform exit)
+  const int n = min(s0 + chunk_tokens, p + 1) - s0;
+  const int chunks_row = min(p / chunk_tokens + 1, num_chunks);
+  const int seq = row_seq[t];
+  const int h0 = kvh * G;
+  const int kv_dim = n_kv_heads * HD;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  for (int i = tid; i < (n + IE_HIP_PAGE_SIZE - 1) / IE_HIP_PAGE_SIZE; i += kThreads) {
+    const int pi = s0 / IE_HIP_PAGE_SIZE + i;
+    const int page = pi < max_pages ? tables[size_t(seq) * max_pages + pi] : -1;
+    pages_s[i] = (page >= 0 && page < num_pages) ? page : 0;
+  }
+  for (int i = tid; i < G * HD; i += kThreads)
+    q_s[i / HD][i % HD] = q[(size_t(t) * n_heads + h0) * HD + i];
+  __syncthreads();
+
+  // 2. scores, one lane per position.
+  float mx[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) mx[g] = -INFINITY;
+  for (int tl = tid; tl < n; tl += kThreads) {
+    const typename K::elem* kr =
+        k_pool + (size_t(pages_s[tl / IE_HIP_PAGE_SIZE]) * IE_HIP_PAGE_SIZE + tl % IE_HIP_PAGE_SIZE) *
+                     kv_dim + kvh * HD;
+    float kk[HD];
+#pragma unroll
+    for (int d8 = 0; d8 < HD / 8; ++d8) K::load8(kr + 8 * d8, kk + 8 * d8);
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+#pragma unroll
+    for (int d4 = 0; d4 < HD / 4; ++d4) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float4 qa = *reinterpret_cast<const float4*>(&q_s[g][4 * d4]);
+        acc[g] = __builtin_fmaf(qa.x, kk[4 * d4 + 0], acc[g]);
+        acc[g] = __builtin_fmaf(qa.y, kk[4 * d4 + 1], acc[g]);
+        acc[g] = __builtin_fmaf(qa.z, kk[4 * d4 + 2], acc[g]);
+        acc[g] = __builtin_fmaf(qa.w, kk[4 * d4 + 3], acc[g]);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float s = acc[g] * scale;
+      scores[g * chunk_tokens + tl] = s;
+      mx[g] = fmaxf(mx[g], s);
+    }
+  }
+
+  // 3. max, then exp and sum, per head.
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float m = wave_max(mx[g]);
+    if (lane == 0) red[wave][g] = m;
+  }
+  __syncthreads();
+  float M[G], ls[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    M[g] = red[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M[g] = fmaxf(M[g], red[w][g]);
+    ls[g] = 0.0f;
+  }
+  if (tid < G) {
+    float m = red[0][tid];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[w][tid]);
+    stat[0][tid] = m;
+  }
+  for (int tl = tid; tl < n; tl += kThreads) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float e = expf(scores[g * chunk_tokens + tl] - M[g]);
+      scores[g * chunk_tokens + tl] = e;
+      ls[g] += e;
+    }
+  }
+  __syncthreads();  // every lane has read `red` (maxima) before it is reused
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float s = wave_sum(ls[g]);
+    if (lane == 0) red[wave][g] = s;
+  }
+  __syncthreads();  // sums and the exp'd scores are visible
+  if (tid < G) {
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) L += red[w][tid];
+    stat[1][tid] = L;
+  }
+
+  // 4. values: lane = (position group pg, dim slice ds), 8 dims per lane.
+  const int pg = lane >> 3, ds = lane & 7;
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[g][u] = 0.0f;
+#pragma unroll 2
+  for (int tl = wave * 8 + pg; tl < n; tl += kWaves * 8) {
+    const typename K::elem* vr =
+        v_pool + (size_t(pages_s[tl / IE_HIP_PAGE_SIZE]) * IE_HIP_PAGE_SIZE + tl % IE_HIP_PAGE_SIZE) *
+                     kv_dim + kvh * HD + ds * 8;
+    float vv[8];
+    K::load8(vr, vv);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float w = scores[g * chunk_tokens + tl];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[g][u] = __builtin_fmaf(w, vv[u], acc[g][u]);
+    }
+  }
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[g][u] += __shfl_xor(acc[g][u], off, 64);
+  if (pg == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) red_o[wave][g][ds * 8 + u] = acc[g][u];
+  }
+  __syncthreads();
+
+  for (int i = tid; i < G * HD; i += kThreads) {
+    const int g = i / HD, d = i % HD;
+    float o = red_o[0][g][d];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) o += red_o[w][g][d];
+    const size_t head = size_t(t) * n_heads + h0 + g;
+    if (chunks_row == 1)
+      out[head * HD + d] = o / stat[1][g];
+    else
+      part_o[(head * num_chunks + c) * HD + d] = o;
+  }
+  if (chunks_row > 1 && tid < G) {
+    const size_t slot = (size_t(t) * n_heads + h0 + tid) * num_chunks + c;
+    part_ml[2 * slot] = stat[0][tid];
+    part_ml[2 * slot + 1] = stat[1][tid];
+  }
+}
+
+// One workgroup per (head, row), one thread per output dim.
+template <int HD>
+__global__ void __launch_bounds__(HD)
+decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
+                    const float* __restrict__ part_ml, const int32_t* __restrict__ row_pos,
+                    int n_heads, int num_chunks, int chunk_tokens) {
+  const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  const int p = row_pos[t];
+  if (p < 0) return;
+  const int nc = min(p / chunk_tokens + 1, num_chunks);
+  if (nc <= 1) return;  // written by the partial kernel
+  const size_t base = (size_t(t) * n_heads + h) * num_chunks;
+  float M = -INFINITY;
+  for (int c = 0; c < nc; ++c) M = fmaxf(M, part_ml[2 * (base + c)]);
+  float L = 0.0f, acc = 0.0f;
+  for (int c = 0; c < nc; ++c) {
+    const float w = expf(part_ml[2 * (base + c)] - M);
+    L = __builtin_fmaf(part_ml[2 * (base + c) + 1], w, L);
+    acc = __builtin_fmaf(part_o[(base + c) * HD + d], w, acc);
+  }
+  out[(size_t(t) * n_heads + h) * HD + d] = acc / L;
+}
+
+template <int KV, int G>
+int launch_valu(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                int num_chunks, int chunk_tokens, const Workspace& ws, int n_heads,
+                int n_kv_heads, hipStream_t stream) {
+  using E = typename Kv<KV>::elem;
+  constexpr int HD = 64;
+  const float scale = 1.0f / sqrtf(float(HD));
+  const size_t lds = size_t(G) * chunk_tokens * sizeof(float);
+  hipLaunchKernelGGL((decode_partial_valu<KV, HD, G>), dim3(T, n_kv_heads, num_chunks),
+                     dim3(kThreads), lds, stream, out, ws.part_o, ws.part_ml, q,
+                     static_cast<const E*>(k_pool), static_cast<const E*>(v_pool), row_pos, row_seq,
+                     kv.tables, kv.max_pages, kv.num_pages, n_heads, n_kv_heads, num_chunks,
+                     chunk_tokens, scale);
+  if (int rc = check_launch("attention_partial")) return rc;
+  if (num_chunks > 1) {
+    hipLaunchKernelGGL((decode_merge_kernel<HD>), dim3(n_heads, T), dim3(HD), 0, stream, out,
+                       ws.part_o, ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
+    if (int rc = check_launch("attention_merge")) return rc;
+  }
+  return IE_HIP_OK;
+}
+
+template <int KV>
+int dispatch_group(int group, float* out, const float* q, const void* k_pool, const void* v_pool,
+                   int T, const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                   int num_chunks, int chunk_tokens, const Workspace& ws, int n_heads,
+                   int n_kv_heads, hipStream_t stream) {
+  switch (group) {
+#define IE_GROUP_CASE(G)                                                                           \
+  case G:                                                                                          \
+    return launch_valu<KV, G>(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks,        \
+                              chunk_tokens, ws, n_heads, n_kv_heads, stream);
+    IE_GROUP_CASE(1)
+    IE_GROUP_CASE(2)
+    IE_GROUP_CASE(3)
+    IE_GROUP_CASE(4)
+    IE_GROUP_CASE(5)
+    IE_GROUP_CASE(6)
+    IE_GROUP_CASE(7)
+    IE_GROUP_CASE(8)
+#undef IE_GROUP_CASE
+  }
+  return fail(IE_HIP_EINVAL, "attention: at most 8 query heads per KV head");
+}
+
+}  // namespace
+
+Workspace carve_workspace(void* base, int T, int n_heads, int head_dim, int num_chunks) {
+  Workspace ws;
+  char* p = static_cast<char*>(base);
+  const size_t slots = size_t(T) * n_heads * num_chunks;
+  ws.part_o = reinterpret_cast<float*>(p);
+  p += align256(slots * head_dim * sizeof(float));
+  ws.part_ml = reinterpret_cast<float*>(p);
+  p += align256(slots * 2 * sizeof(float));
+  ws.counters = reinterpret_cast<int32_t*>(p);
+  return ws;
+}
+
+size_t workspace_bytes(int T, int n_heads, int head_dim, int num_chunks) {
+  const size_t slots = size_t(T) * n_heads * num_chunks;
+  return align256(slots * head_dim * sizeof(float)) + align256(slots * 2 * sizeof(float)) +
+         align256(size_t(T) * sizeof(int32_t));
+}
+
+int device_compute_units() {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+      (void)hipGetLastError();
+      return 256;  // MI355X
+    }
+    return n;
+  }();
+  return cus;
+}
+
+int decode_valu(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
+                hipStream_t stream) {
+  const int group = n_heads / n_kv_heads;
+  const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
+  switch (kv.kv_dtype) {
+    case IE_KV_F32:
+      return dispatch_group<IE_KV_F32>(group, out, q, k_pool, v_pool, T, row_pos, row_seq, kv,
+                                       num_chunks, chunk_tokens, ws, n_heads, n_kv_heads, stream);
+    case IE_KV_F16:
+      return dispatch_group<IE_KV_F16>(group, out, q, k_pool, v_pool, T, row_pos, row_seq, kv,
+                                       num_chunks, chunk_tokens, ws, n_heads, n_kv_heads, stream);
+    case IE_KV_BF16:
+      return dispatch_group<IE_KV_BF16>(group, out, q, k_pool, v_pool, T, row_pos, row_seq, kv,
+                                        num_chunks, chunk_tokens, ws, n_heads, n_kv_heads, stream);
+  }
+  return fail(IE_HIP_EINVAL, "attention: unsupported kv_dtype");
+}
+
+}  // namespace iehip
+
+using namespace iehip;
+
+extern "C" {
+
+int ie_hip_attention_chunks(int context_tokens, int chunk_tokens) {
+  if (context_tokens <= 0 || chunk_tokens <= 0) return 0;
+  return (context_tokens + chunk_tokens - 1) / chunk_tokens;
+}
+
+int ie_hip_attention_chunk_tokens(int T, int max_context) {
+  const int cus = device_compute_units();
+  for (int ct : {512, 256, 128, 64})
+    if (int64_t(std::max(T, 1)) * ie_hip_attention_chunks(std::max(max_context, 1), ct) >= cus)
+      return ct;
+  return 64;
+}
+
+size_t ie_hip_attention_workspace_bytes(int T, int n_heads, int head_dim, int num_chunks) {
+  if (T <= 0 || n_heads <= 0 || head_dim <= 0 || num_chunks <= 0) return 0;
+  return workspace_bytes(T, n_heads, head_dim, num_chunks);
+}
+
+int ie_hip_attention(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                     const int32_t* row_pos, const int32_t* row_seq, ie_kv_layout kv,
+                     int num_chunks, int chunk_tokens, void* workspace, int n_heads,
+                     int n_kv_heads, int head_dim, hipStream_t stream) {
+  clear_error();
+  if (int rc = check_layout(kv, "attention")) return rc;
+  if (head_dim != 64) return fail(IE_HIP_EINVAL, "attention: head_dim must be 64");
+  if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads / n_kv_heads > 8)
+    return fail(IE_HIP_EINVAL, "attention: at most 8 query heads per KV head");
+  if (chunk_tokens < IE_HIP_PAGE_SIZE || chunk_tokens > 1024 || chunk_tokens % IE_HIP_PAGE_SIZE)
+    return fail(IE_HIP_EINVAL, "attention: chunk_tokens must be a multiple of 16 in [16, 1024]");
+  if (num_chunks <= 0 || T < 0) return fail(IE_HIP_EINVAL, "attention: bad chunk or row count");
+  if (T == 0) return IE_HIP_OK;
+  if (!out || !q || !k_pool || !v_pool || !row_pos || !row_seq || !workspace)
+    return fail(IE_HIP_EINVAL, "attention: null pointer");
+  return decode_valu(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
+                     workspace, n_heads, n_kv_heads, stream);
+}
+
+}  // extern "C"

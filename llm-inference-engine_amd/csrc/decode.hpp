@@ -1,0 +1,29 @@
+// Internal interface of the decode-attention kernels.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "ie_hip.h"
+
+namespace iehip {
+
+inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// The caller-owned decode workspace, carved into its parts.
+struct Workspace {
+  float* part_o = nullptr;     // [T][n_heads][num_chunks][head_dim] unnormalised partial outputs
+  float* part_ml = nullptr;    // [T][n_heads][num_chunks][2] partial max and sum of exp
+  int32_t* counters = nullptr; // [T] finished-chunk counters (zero between calls)
+};
+
+Workspace carve_workspace(void* base, int T, int n_heads, int head_dim, int num_chunks);
+size_t workspace_bytes(int T, int n_heads, int head_dim, int num_chunks);
+int device_compute_units();
+
+int decode_valu(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
+                hipStream_t stream);
+
+}  // namespace iehip

@@ -1,0 +1,20 @@
+// Internal interface of the prefill-attention kernels.
+#pragma once
+
+#include <cstdint>
+
+#include "ie_hip.h"
+
+namespace iehip {
+
+int prefill_valu_launch(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                        const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                        int n_heads, int n_kv_heads, hipStream_t stream);
+
+// 16-bit KV caches: QK^T and PV on MFMA (prefill_mfma.hip).
+bool prefill_mfma_enabled();
+int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                        const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                        int n_heads, int n_kv_heads, hipStream_t stream);
+
+}  // namespace iehip

@@ -1,0 +1,166 @@
+"""Flash-decoding attention over pages on the GPU vs the CPU oracle.
+
+Tolerances (north star): f32 KV -- the reference's metric max|d| / max|ref|
+(src/npy.cpp:98-110) <= 1e-5; f16 / bf16 KV -- max |d| <= 2e-3 absolute. The
+oracle attends over the same 16-bit values widened to f32. Outputs must also
+be finite (the reference metric lets a NaN through unless it is last).
+Cases: the golden fixtures (made from the reference's own CPU code), the
+reference self-test's cases (src/cuda/cuda_runner.cu:914-941) including extra
+empty chunks, several chunk sizes, and BASELINE config 3 at full size.
+"""
+from __future__ import annotations
+
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import HD, KVD, NH, NKV, QD, from_dev, kv_pool, make_tables, normal, to_dev
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+KVS = {"f32": 0, "f16": 1, "bf16": 2}
+F32_REL, HALF_ABS = 1e-5, 2e-3
+
+
+def check(O, got, want, kvt, what=""):
+    assert np.all(np.isfinite(got)), f"non-finite output {what}"
+    if kvt == 0:
+        rel = O.compare(got, want)[0]
+        assert rel <= F32_REL, f"rel err {rel:.3e} {what}"
+    else:
+        err = float(np.abs(got - want).max())
+        assert err <= HALF_ABS, f"abs err {err:.3e} {what}"
+
+
+def gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, chunk_tokens,
+                  num_chunks=None):
+    T = len(row_pos)
+    if num_chunks is None:
+        num_chunks = ie.attention_chunks(int(np.max(row_pos)) + 1, chunk_tokens)
+    ws = ie.attention_workspace(T, NH, HD, num_chunks)
+    out = torch.full((T, QD), float("nan"), dtype=torch.float32, device=dev)
+    ie.attention(out, to_dev(q, dev), to_dev(kp, dev, kvt), to_dev(vp, dev, kvt),
+                 to_dev(row_pos, dev), to_dev(row_seq, dev), to_dev(tables, dev), max_pages,
+                 num_chunks, chunk_tokens, ws, NH, NKV, HD)
+    torch.cuda.synchronize()
+    return from_dev(out)
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "attn_*.npz"))),
+                         ids=lambda p: os.path.basename(p)[5:-4])
+@pytest.mark.parametrize("kv", list(KVS))
+def test_golden(ie, O, dev, path, kv):
+    g = np.load(path)
+    kvt = KVS[kv]
+    tables, max_pages = g["tables"], g["tables"].shape[1]
+    kf, vf = O.widen_kv(g["k_pool_f16"], 1), O.widen_kv(g["v_pool_f16"], 1)
+    kp, vp = O.round_to_kv(kf, kvt), O.round_to_kv(vf, kvt)
+    if kvt == 2:  # bf16 pools hold different values: the oracle recomputes the expectation
+        want = O.paged_attention(g["q"], kp, vp, kvt, g["row_pos"], g["row_seq"], tables, max_pages,
+                                 NH, NKV, HD)
+    else:
+        want = g["out"]
+    for ct in (16, 64, 512):
+        got = gpu_attention(ie, dev, g["q"], kp, vp, kvt, g["row_pos"], g["row_seq"], tables,
+                            max_pages, ct)
+        check(O, got, want, kvt, f"chunk {ct}")
+
+
+SELFTEST = [
+    # lens, rows, capacity (the launch covers `capacity` positions: extra chunks are empty)
+    ([1], [(0, 0)], 1),
+    ([64], [(0, 63)], 64),
+    ([65], [(0, 64)], 1000),
+    ([256], [(0, 255)], 256),
+    ([257], [(0, 256)], 4096),
+    ([3000], [(0, 2999)], 3000),
+    ([540], [(0, p) for p in range(500, 540)], 540),
+    ([6, 17, 256, 257, 3000], [(0, 5), (1, 16), (2, 255), (3, 256), (4, 2999)], 4096),
+    ([101, 30, 1001], [(0, 100), (2, 1000)] + [(1, p) for p in range(30)], 1024),
+]
+
+
+@pytest.mark.parametrize("case", range(len(SELFTEST)))
+@pytest.mark.parametrize("kv", list(KVS))
+@pytest.mark.parametrize("chunk_tokens", [64, 256, 512])
+def test_selftest_cases(ie, O, dev, case, kv, chunk_tokens):
+    lens, rows, capacity = SELFTEST[case]
+    kvt = KVS[kv]
+    rng = np.random.default_rng(100 + case)
+    tables, max_pages, num_pages = make_tables(lens, rng, extra_pages=3)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_seq = np.array([r[0] for r in rows], np.int32)
+    row_pos = np.array([r[1] for r in rows], np.int32)
+    q = normal(rng, (len(rows), QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
+                             threads=8)
+    nc = ie.attention_chunks(capacity, chunk_tokens)
+    got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, chunk_tokens,
+                        num_chunks=nc)
+    check(O, got, want, kvt, f"case {case}")
+
+
+def test_page_permutation_invariance(ie, O, dev):
+    """The same logical K/V under two page permutations gives the same output (bit-exact:
+    the kernel's arithmetic depends only on positions, not on where pages live)."""
+    rng = np.random.default_rng(7)
+    L, kvt = 1500, 1
+    logical_k = kv_pool(rng, (L + 15) // 16, kvt, O)
+    logical_v = kv_pool(rng, (L + 15) // 16, kvt, O)
+    q = normal(rng, (1, QD))
+    outs = []
+    for seed in (1, 2):
+        tables, max_pages, num_pages = make_tables([L], np.random.default_rng(seed), extra_pages=4)
+        kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+        for p in range(L):
+            kp[tables[0, p // 16] * 16 + p % 16] = logical_k[p]
+            vp[tables[0, p // 16] * 16 + p % 16] = logical_v[p]
+        outs.append(gpu_attention(ie, dev, q, kp, vp, kvt, np.array([L - 1], np.int32),
+                                  np.zeros(1, np.int32), tables, max_pages, 256))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+def test_chunk_size_invariance(ie, O, dev):
+    """Split-K partition size changes only rounding (log-sum-exp merge is exact)."""
+    rng = np.random.default_rng(8)
+    lens = [4096, 129, 2000]
+    tables, max_pages, num_pages = make_tables(lens, rng)
+    kvt = 1
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_pos = np.array([n - 1 for n in lens], np.int32)
+    row_seq = np.arange(len(lens), dtype=np.int32)
+    q = normal(rng, (len(lens), QD))
+    outs = [gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct)
+            for ct in (16, 128, 1024)]
+    assert np.abs(outs[0] - outs[1]).max() < 2e-6 and np.abs(outs[0] - outs[2]).max() < 2e-6
+
+
+@pytest.mark.parametrize("kv", ["f16", "f32"])
+def test_config3_full_size(ie, O, dev, kv):
+    """batch 64, L ~ U[128, 4096], 16-token pages, tables a seeded
+    permutation of a 65,536-page pool, 512-token partitions."""
+    rng = np.random.default_rng(20263)
+    kvt = KVS[kv]
+    num_pages = 65536
+    lens = rng.integers(128, 4097, 64)
+    max_pages = 4096 // 16
+    perm = rng.permutation(num_pages).astype(np.int32)
+    tables = np.zeros((64, max_pages), np.int32)
+    nxt = 0
+    for s, n in enumerate(lens):
+        k = (int(n) + 15) // 16
+        tables[s, :k] = perm[nxt:nxt + k]
+        nxt += k
+    kp = kv_pool(rng, num_pages, kvt, O)
+    vp = kv_pool(rng, num_pages, kvt, O)
+    row_pos = (lens - 1).astype(np.int32)
+    row_seq = np.arange(64, dtype=np.int32)
+    q = normal(rng, (64, QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
+                             threads=8)
+    got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, 512,
+                        num_chunks=8)
+    check(O, got, want, kvt, "config 3")

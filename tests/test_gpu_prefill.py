@@ -1,0 +1,104 @@
+"""Prefill (prompt-chunk) attention into pages on the GPU vs the CPU oracle.
+
+Same tolerances as decode (f32: rel 1e-5; f16/bf16: 2e-3 abs). Cases: the
+reference self-test's prompts (src/cuda/cuda_runner.cu:920-934: 1, 17, 300,
+1000 rows; a prompt continuing at 500; the 2nd of 2 sequences) and the
+4,000-token prefill of BASELINE config 5, appended into fresh pages of a
+churned pool with the fused RoPE+append kernel first (rows sampled for the
+oracle). Decode and prefill kernels must agree on the same rows.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import HD, KVD, NH, NKV, QD, THETA, from_dev, kv_pool, make_tables, normal, to_dev
+from test_gpu_decode import check, gpu_attention
+
+pytestmark = pytest.mark.gpu
+KVS = {"f32": 0, "f16": 1, "bf16": 2}
+
+
+def gpu_prefill(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages):
+    out = torch.full((len(row_pos), QD), float("nan"), dtype=torch.float32, device=dev)
+    ie.attention_prefill(out, to_dev(q, dev), to_dev(kp, dev, kvt), to_dev(vp, dev, kvt),
+                         to_dev(row_pos, dev), to_dev(row_seq, dev), to_dev(tables, dev), max_pages,
+                         NH, NKV, HD)
+    torch.cuda.synchronize()
+    return from_dev(out)
+
+
+PROMPTS = [
+    ([1], 0, 0, 1),
+    ([17], 0, 0, 17),
+    ([300], 0, 0, 300),
+    ([1000], 0, 0, 1000),
+    ([540], 0, 500, 40),          # a prompt continuing at 500
+    ([100, 300], 1, 0, 300),     # the 2nd of 2 sequences
+    ([129], 0, 63, 66),          # starts mid-tile, crosses tile edges
+]
+
+
+@pytest.mark.parametrize("case", range(len(PROMPTS)))
+@pytest.mark.parametrize("kv", list(KVS))
+def test_prompts(ie, O, dev, case, kv):
+    lens, seq, start, T = PROMPTS[case]
+    kvt = KVS[kv]
+    rng = np.random.default_rng(200 + case)
+    tables, max_pages, num_pages = make_tables(lens, rng, extra_pages=2)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_pos = np.arange(start, start + T, dtype=np.int32)
+    row_seq = np.full(T, seq, np.int32)
+    q = normal(rng, (T, QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
+                             threads=8)
+    got = gpu_prefill(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages)
+    check(O, got, want, kvt, f"prompt case {case}")
+    dec = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, 256)
+    check(O, dec, want, kvt, f"decode kernel on prompt case {case}")
+
+
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_config5_prefill_4000_into_churned_pool(ie, O, dev, kv):
+    """BASELINE config 5 (prefill half): 25% of a pool's pages freed and re-allocated from a
+    seeded free list, then a 4,000-token chunk appended into fresh pages (RoPE+append kernel)
+    and attended causally. Pages are checked bit-exactly; attention on sampled rows."""
+    kvt = KVS[kv]
+    rng = np.random.default_rng(20265)
+    num_pages, T = 8192, 4000
+    pool = ie.PagePool(num_pages, 64, 8192)
+    seqs = [pool.open_sequence() for _ in range(48)]
+    for s in seqs:
+        pool.ensure(s, int(rng.integers(256, 2049)))
+    for s in rng.permutation(seqs)[:12]:  # 25% of the decode sequences finish
+        pool.close_sequence(int(s))
+    p = pool.open_sequence()
+    pool.ensure(p, T)
+    max_pages = pool.max_pages_per_seq
+    tables = np.array(pool.host_tables(), np.int32).reshape(pool.max_batch, max_pages)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    q = normal(rng, (T, QD))
+    k = normal(rng, (T, KVD))
+    v = normal(rng, (T, KVD))
+    row_pos = np.arange(T, dtype=np.int32)
+    row_seq = np.full(T, p, np.int32)
+    q_rot, kp_ref, vp_ref = O.rope_append_paged(q, k, v, kp, vp, kvt, row_pos, row_seq, tables,
+                                                max_pages, NH, NKV, HD, THETA)
+    dq = to_dev(q, dev)
+    dkp, dvp = to_dev(kp, dev, kvt), to_dev(vp, dev, kvt)
+    dtab = torch.zeros(tables.size, dtype=torch.int32, device=dev)
+    assert pool.upload_tables(dtab)
+    table = ie.rope_table(8192, HD, THETA).to(dev)
+    dpos, dseq = to_dev(row_pos, dev), to_dev(row_seq, dev)
+    ie.rope_and_cache(dq, to_dev(k, dev), to_dev(v, dev), dkp, dvp, table, dpos, dseq, dtab,
+                      max_pages, NH, NKV, HD)
+    out = torch.full((T, QD), float("nan"), dtype=torch.float32, device=dev)
+    ie.attention_prefill(out, dq, dkp, dvp, dpos, dseq, dtab, max_pages, NH, NKV, HD)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(dq).view(np.uint32), q_rot.view(np.uint32))
+    assert np.array_equal(from_dev(dkp), kp_ref) and np.array_equal(from_dev(dvp), vp_ref)
+    sample = np.unique(np.concatenate([[0, 1, 15, 16, 63, 64, T - 1], rng.integers(0, T, 25)]))
+    want = O.paged_attention(q_rot[sample], kp_ref, vp_ref, kvt, row_pos[sample], row_seq[sample],
+                             tables, max_pages, NH, NKV, HD, threads=8)
+    check(O, from_dev(out)[sample], want, kvt, "config 5 prefill")
