@@ -268,6 +268,7 @@ def main():
     ap.add_argument("--kv", choices=list(KV_CODES), default=None)
     ap.add_argument("--chunk-tokens", type=int, default=None)
     ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--impl", choices=["auto", "valu", "mfma"], default="auto")
     ap.add_argument("--seed", type=int, default=20263)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -286,6 +287,7 @@ def main():
 
     ie = g.load()
     ie.lib()
+    ie.set_attention_impl({"auto": ie.IMPL_AUTO, "valu": ie.IMPL_VALU, "mfma": ie.IMPL_MFMA}[args.impl])
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
     res = bench_decode(args, torch, ie, O) if args.config == 3 else bench_append(args, torch, ie, O)

@@ -61,6 +61,17 @@ const char* ie_hip_last_error(void);
 /* Library version string and the device it was built for ("gfx950"). */
 const char* ie_hip_version(void);
 
+/* Process-wide choice of attention kernels, like the reference's kernel
+ * switches (set_tensor_cores / set_tc_fp16, src/cuda/kernels.cuh:113-118):
+ *   IE_HIP_IMPL_AUTO (default) -- matrix-core (MFMA) kernels wherever the
+ *       shape and KV type allow them, the VALU kernels otherwise;
+ *   IE_HIP_IMPL_VALU -- always the float32 VALU kernels (for comparison);
+ *   IE_HIP_IMPL_MFMA -- MFMA kernels only; unsupported shapes fail with EINVAL.
+ * Returns the previous setting. Not synchronised with running kernels: set it
+ * before launching. */
+enum { IE_HIP_IMPL_AUTO = 0, IE_HIP_IMPL_VALU = 1, IE_HIP_IMPL_MFMA = 2 };
+int ie_hip_set_attention_impl(int impl);
+
 /* ---------------------------------------------------------------- RoPE ---
  * Host-side RoPE table, computed with the host C library exactly as the
  * reference's CPU rope does (src/ops.cpp:37-48): for p < n_pos, i < head_dim/2,

@@ -47,6 +47,7 @@ _vp, _i, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
 _SIGS = {
     "ie_hip_last_error": (ctypes.c_char_p, []),
     "ie_hip_version": (ctypes.c_char_p, []),
+    "ie_hip_set_attention_impl": (_i, [_i]),
     "ie_hip_rope_table": (_i, [_vp, _i, _i, _f]),
     "ie_hip_rope_and_cache": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, KvLayout, _i, _i,
                                    _i, _vp]),
@@ -129,6 +130,14 @@ def layout(tables, max_pages: int, num_pages: int, kv_dtype: int) -> KvLayout:
 def torch_kv_dtype(kv_dtype: int):
     import torch
     return {KV_F32: torch.float32, KV_F16: torch.float16, KV_BF16: torch.bfloat16}[kv_dtype]
+
+
+IMPL_AUTO, IMPL_VALU, IMPL_MFMA = 0, 1, 2
+
+
+def set_attention_impl(impl: int) -> int:
+    """Process-wide attention kernel choice (AUTO / VALU / MFMA); returns the previous one."""
+    return int(lib().ie_hip_set_attention_impl(impl))
 
 
 # ------------------------------------------------------------ kernels ----

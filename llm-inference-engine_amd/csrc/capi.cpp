@@ -5,6 +5,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "decode.hpp"
 
 namespace iehip {
 
@@ -32,6 +33,12 @@ int check_launch(const char* kernel) {
               std::string("HIP kernel ") + kernel + " failed to launch: " + hipGetErrorString(err));
 }
 
+namespace {
+int g_attention_impl = IE_HIP_IMPL_AUTO;
+}
+
+int attention_impl() { return g_attention_impl; }
+
 int check_layout(const ie_kv_layout& kv, const char* who) {
   if (kv.page_size != IE_HIP_PAGE_SIZE)
     return fail(IE_HIP_EINVAL, std::string(who) + ": KV page size must be 16");
@@ -51,6 +58,13 @@ extern "C" {
 const char* ie_hip_last_error(void) { return g_last_error.c_str(); }
 
 const char* ie_hip_version(void) { return "ie_hip 0.1 (gfx950, wave64)"; }
+
+int ie_hip_set_attention_impl(int impl) {
+  const int prev = g_attention_impl;
+  if (impl == IE_HIP_IMPL_AUTO || impl == IE_HIP_IMPL_VALU || impl == IE_HIP_IMPL_MFMA)
+    g_attention_impl = impl;
+  return prev;
+}
 
 // The angle and cos/sin of src/ops.cpp:37-48, evaluated with the host libm so
 // the table equals what the reference CPU rope computes for every position.

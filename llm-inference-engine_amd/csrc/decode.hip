@@ -248,12 +248,7 @@ int launch_valu(float* out, const float* q, const void* k_pool, const void* v_po
                      kv.tables, kv.max_pages, kv.num_pages, n_heads, n_kv_heads, num_chunks,
                      chunk_tokens, scale);
   if (int rc = check_launch("attention_partial")) return rc;
-  if (num_chunks > 1) {
-    hipLaunchKernelGGL((decode_merge_kernel<HD>), dim3(n_heads, T), dim3(HD), 0, stream, out,
-                       ws.part_o, ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
-    if (int rc = check_launch("attention_merge")) return rc;
-  }
-  return IE_HIP_OK;
+  return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
 }
 
 template <int KV>
@@ -280,6 +275,14 @@ int dispatch_group(int group, float* out, const float* q, const void* k_pool, co
 }
 
 }  // namespace
+
+int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T, int n_heads,
+                 int num_chunks, int chunk_tokens, hipStream_t stream) {
+  if (num_chunks <= 1) return IE_HIP_OK;
+  hipLaunchKernelGGL((decode_merge_kernel<64>), dim3(n_heads, T), dim3(64), 0, stream, out,
+                     ws.part_o, ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
+  return check_launch("attention_merge");
+}
 
 Workspace carve_workspace(void* base, int T, int n_heads, int head_dim, int num_chunks) {
   Workspace ws;
@@ -372,6 +375,15 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
   if (T == 0) return IE_HIP_OK;
   if (!out || !q || !k_pool || !v_pool || !row_pos || !row_seq || !workspace)
     return fail(IE_HIP_EINVAL, "attention: null pointer");
+  const int impl = attention_impl();
+  if (impl != IE_HIP_IMPL_VALU &&
+      decode_mfma_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens))
+    return decode_mfma(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
+                       workspace, n_heads, n_kv_heads, stream);
+  if (impl == IE_HIP_IMPL_MFMA)
+    return fail(IE_HIP_EINVAL, "attention: the MFMA kernel does not support this shape "
+                               "(16-bit KV, kv_dim <= 128, n_heads <= 16, chunk a multiple of 64 "
+                               "up to 512)");
   return decode_valu(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
                      workspace, n_heads, n_kv_heads, stream);
 }

@@ -21,6 +21,19 @@ Workspace carve_workspace(void* base, int T, int n_heads, int head_dim, int num_
 size_t workspace_bytes(int T, int n_heads, int head_dim, int num_chunks);
 int device_compute_units();
 
+int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T, int n_heads,
+                 int num_chunks, int chunk_tokens, hipStream_t stream);
+
+// Process-wide kernel choice (ie_hip_set_attention_impl).
+int attention_impl();
+
+bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim,
+                           int chunk_tokens);
+int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
+                hipStream_t stream);
+
 int decode_valu(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                 const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,

@@ -16,6 +16,7 @@
 
 #include "common.hpp"
 #include "prefill.hpp"
+#include "decode.hpp"
 
 namespace iehip {
 namespace {
@@ -189,7 +190,7 @@ int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, con
   if (T == 0) return IE_HIP_OK;
   if (!out || !q || !k_pool || !v_pool || !row_pos || !row_seq)
     return fail(IE_HIP_EINVAL, "attention_prefill: null pointer");
-  if (kv.kv_dtype != IE_KV_F32 && prefill_mfma_enabled())
+  if (kv.kv_dtype != IE_KV_F32 && attention_impl() != IE_HIP_IMPL_VALU && prefill_mfma_enabled())
     return prefill_mfma_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads,
                                n_kv_heads, stream);
   return prefill_valu_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads, n_kv_heads,

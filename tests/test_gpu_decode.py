@@ -35,6 +35,14 @@ def check(O, got, want, kvt, what=""):
         assert err <= HALF_ABS, f"abs err {err:.3e} {what}"
 
 
+@pytest.fixture(params=["auto", "valu"])
+def impl(request, ie):
+    """Runs a test with the default kernels (MFMA for 16-bit caches) and with the VALU ones."""
+    prev = ie.set_attention_impl({"auto": ie.IMPL_AUTO, "valu": ie.IMPL_VALU}[request.param])
+    yield request.param
+    ie.set_attention_impl(prev)
+
+
 def gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, chunk_tokens,
                   num_chunks=None):
     T = len(row_pos)
@@ -52,7 +60,7 @@ def gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, 
 @pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "attn_*.npz"))),
                          ids=lambda p: os.path.basename(p)[5:-4])
 @pytest.mark.parametrize("kv", list(KVS))
-def test_golden(ie, O, dev, path, kv):
+def test_golden(ie, O, dev, path, kv, impl):
     g = np.load(path)
     kvt = KVS[kv]
     tables, max_pages = g["tables"], g["tables"].shape[1]
@@ -86,7 +94,7 @@ SELFTEST = [
 @pytest.mark.parametrize("case", range(len(SELFTEST)))
 @pytest.mark.parametrize("kv", list(KVS))
 @pytest.mark.parametrize("chunk_tokens", [64, 256, 512])
-def test_selftest_cases(ie, O, dev, case, kv, chunk_tokens):
+def test_selftest_cases(ie, O, dev, case, kv, chunk_tokens, impl):
     lens, rows, capacity = SELFTEST[case]
     kvt = KVS[kv]
     rng = np.random.default_rng(100 + case)
@@ -103,7 +111,7 @@ def test_selftest_cases(ie, O, dev, case, kv, chunk_tokens):
     check(O, got, want, kvt, f"case {case}")
 
 
-def test_page_permutation_invariance(ie, O, dev):
+def test_page_permutation_invariance(ie, O, dev, impl):
     """The same logical K/V under two page permutations gives the same output (bit-exact:
     the kernel's arithmetic depends only on positions, not on where pages live)."""
     rng = np.random.default_rng(7)
@@ -123,7 +131,7 @@ def test_page_permutation_invariance(ie, O, dev):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
-def test_chunk_size_invariance(ie, O, dev):
+def test_chunk_size_invariance(ie, O, dev, impl):
     """Split-K partition size changes only rounding (log-sum-exp merge is exact)."""
     rng = np.random.default_rng(8)
     lens = [4096, 129, 2000]
@@ -134,12 +142,12 @@ def test_chunk_size_invariance(ie, O, dev):
     row_seq = np.arange(len(lens), dtype=np.int32)
     q = normal(rng, (len(lens), QD))
     outs = [gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct)
-            for ct in (16, 128, 1024)]
+            for ct in (64, 128, 512)]
     assert np.abs(outs[0] - outs[1]).max() < 2e-6 and np.abs(outs[0] - outs[2]).max() < 2e-6
 
 
 @pytest.mark.parametrize("kv", ["f16", "f32"])
-def test_config3_full_size(ie, O, dev, kv):
+def test_config3_full_size(ie, O, dev, kv, impl):
     """batch 64, L ~ U[128, 4096], 16-token pages, tables a seeded
     permutation of a 65,536-page pool, 512-token partitions."""
     rng = np.random.default_rng(20263)
@@ -164,3 +172,22 @@ def test_config3_full_size(ie, O, dev, kv):
     got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, 512,
                         num_chunks=8)
     check(O, got, want, kvt, "config 3")
+
+
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_mfma_forced_and_shape_limits(ie, O, dev, kv):
+    """IMPL_MFMA runs the matrix-core kernel; shapes it cannot take fail loudly (no silent fallback)."""
+    kvt = KVS[kv]
+    rng = np.random.default_rng(9)
+    tables, max_pages, num_pages = make_tables([700], rng)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    q = normal(rng, (1, QD))
+    pos, seq = np.array([699], np.int32), np.zeros(1, np.int32)
+    want = O.paged_attention(q, kp, vp, kvt, pos, seq, tables, max_pages, NH, NKV, HD)
+    prev = ie.set_attention_impl(ie.IMPL_MFMA)
+    try:
+        check(O, gpu_attention(ie, dev, q, kp, vp, kvt, pos, seq, tables, max_pages, 128), want, kvt)
+        with pytest.raises(ie.IeHipError):
+            gpu_attention(ie, dev, q, kp, vp, kvt, pos, seq, tables, max_pages, 48)
+    finally:
+        ie.set_attention_impl(prev)
