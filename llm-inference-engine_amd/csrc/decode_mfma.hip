@@ -1,6 +1,6 @@
 // Flash-decoding attention over pages on the matrix cores (gfx950), for f16
-// and bf16 KV caches whose rows hold at most 128 elements (n_kv_heads * 64)
-// and at most 16 query heads -- Qwen2.5-0.5B: 14 query heads, 2 KV heads.
+// and bf16 KV caches whose rows hold 128 elements (2 KV heads x 64) and at
+// most 16 query heads -- Qwen2.5-0.5B: 14 query heads, 2 KV heads.
 //
 // Reference semantics: each row's causal GQA attention, src/ops.cpp:70-108;
 // split-K chunks merged by log-sum-exp as in src/cuda/kernels.cu:309-507.
@@ -23,17 +23,19 @@
 // Layout of the work:
 //   grid (T, num_chunks), rows fastest; chunk_tokens / 64 (<= 8) waves per workgroup,
 //   each wave owns 64 consecutive positions = 4 pages = 2 page pairs.
-//   1. K: each lane loads its token row's 16-byte pieces straight into the MFMA
-//      A-operand registers (4 x global_load_dwordx4 per page; lanes 0-15 hold
-//      tokens 0-15, the 4 lane groups hold the 4 16-byte slices of each 64-byte
-//      quarter row). 8 MFMA 16x16x32 per page.
+//   1. All K and V loads of the wave are issued first (one memory round trip).
+//      K goes straight into the MFMA A-operand registers (4 x 16-byte loads per
+//      page; lanes 0-15 hold tokens 0-15, the 4 lane groups hold the 4 16-byte
+//      slices of each 64-byte quarter row). 8 MFMA 16x16x32 per page.
 //   2. softmax over the chunk: wave-local max/sum by shuffles, across waves
 //      through LDS (scores kept in registers; base-2 exponent).
 //   3. V: each page pair (8 KB) is staged in a per-wave LDS tile with 16-byte
 //      coalesced loads and read back transposed (one 2-byte element per lane per
 //      slot) as the B operand; 16 MFMA 16x16x32 per pair.
 //   4. O: per-wave tiles summed through LDS; a row whose context fits one chunk
-//      writes `out` directly, otherwise the chunk writes (o, m, l) for the merge.
+//      writes `out` directly, otherwise the chunk writes (o, m, l) and the last
+//      chunk of the row to finish merges them (atomic counter per row in the
+//      workspace, reset by that chunk): one launch, no separate merge kernel.
 #include "common.hpp"
 #include "decode.hpp"
 
@@ -45,11 +47,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKvd = 128;                 // elements per KV row (n_kv_heads * 64)
-constexpr int kVStride = kKvd + 4;        // LDS row stride of a staged V pair (halfs)
-constexpr int kVTileHalfs = 32 * kVStride;  // one page pair
+constexpr int kWaveLds = 16384;           // per-wave LDS: two 8 KB V page-pair tiles
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kMaxLds = 8 * (kVTileHalfs * 2 + 16 * 2 * 4);  // 8 waves
+constexpr int kMaxLds = 8 * (kWaveLds + 16 * 2 * 4);  // 8 waves
 
 template <int KV>
 struct Mfma;
@@ -75,19 +76,21 @@ struct Mfma<IE_KV_BF16> {
 template <int KV>
 __global__ void __launch_bounds__(512)
 decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
-                    float* __restrict__ part_ml, const float* __restrict__ q,
-                    const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
-                    const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
-                    const int32_t* __restrict__ tables, int max_pages, int num_pages, int n_heads,
-                    int group, int kv_dim, int num_chunks, int chunk_tokens) {
+                    float* __restrict__ part_ml, int32_t* __restrict__ counters,
+                    const float* __restrict__ q, const uint16_t* __restrict__ k_pool,
+                    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ row_pos,
+                    const int32_t* __restrict__ row_seq, const int32_t* __restrict__ tables,
+                    int max_pages, int num_pages, int n_heads, int group, int num_chunks,
+                    int chunk_tokens) {
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_last;
   const int waves = blockDim.x >> 6;
-  // LDS: per-wave V tile / O tile, then per-wave head maxima and sums.
-  E* vtile_all = reinterpret_cast<E*>(smem);
-  float* red_m = reinterpret_cast<float*>(smem + size_t(waves) * kVTileHalfs * sizeof(E));
+  // LDS: per wave a 16 KB V area (two 8 KB page-pair tiles, later the O tile),
+  // then per-wave head maxima and sums.
+  float* red_m = reinterpret_cast<float*>(smem + size_t(waves) * kWaveLds);
   float* red_l = red_m + waves * 16;
 
   const int t = blockIdx.x, c = blockIdx.y;
@@ -99,11 +102,12 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   const int seq = row_seq[t];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
-  const int wt0 = wave * 64;  // first position of this wave within the chunk
-  const int ks_count = kv_dim / 32;
+  const int wt0 = wave * 64;      // first position of this wave within the chunk
+  const bool active = wt0 < n;    // wave-uniform: the wave has positions to read
+  unsigned char* warea = smem + size_t(wave) * kWaveLds;
 
-  // Page ids of this wave's 4 pages; pages past the context (or outside the
-  // pool) are not loaded, and their positions are masked.
+  // Page ids of this wave's 4 pages. A page past the context or outside the
+  // pool is replaced by the wave's first page (re-read from cache, masked).
   int page[4];
   bool page_ok[4];
 #pragma unroll
@@ -113,8 +117,41 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     int id = -1;
     if (first < n && pi < max_pages) id = tables[size_t(seq) * max_pages + pi];
     page_ok[pg] = id >= 0 && id < num_pages;
-    page[pg] = page_ok[pg] ? id : 0;
+    page[pg] = id;
   }
+#pragma unroll
+  for (int pg = 0; pg < 4; ++pg)
+    if (!page_ok[pg]) page[pg] = page_ok[0] ? page[0] : 0;
+
+  // 1. Every load of the wave is issued before any math (one memory round trip):
+  //    V straight into LDS by DMA (global_load_lds_dwordx4: lane l of a load lands
+  //    at base + 16 l), K into the MFMA A-operand registers (lane (g, r): token r
+  //    of the page, 16-byte slice g of each 64-byte quarter row).
+  //    V tile of a page pair: 32 rows of 256 bytes, 16-byte piece k of row `tok`
+  //    stored at slot k ^ 2*((tok >> 2) & 3), so the transposed reads below hit
+  //    four different bank groups for the four lane groups.
+  op ka[4][4];
+  if (active) {
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int tok = 4 * u + (lane >> 4);                    // 0..31 within the pair
+        const int piece = (lane & 15) ^ (2 * (u & 3));          // global piece for slot lane&15
+        const uint16_t* src = v_pool +
+            (size_t(page[2 * pp + (tok >> 4)]) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece;
+        __builtin_amdgcn_global_load_lds(
+            (const void __attribute__((address_space(1)))*)(src),
+            (void __attribute__((address_space(3)))*)(warea + pp * 8192 + u * 1024), 16, 0, 0);
+      }
+#pragma unroll
+    for (int pg = 0; pg < 4; ++pg) {
+      const uint16_t* krow = k_pool + (size_t(page[pg]) * IE_HIP_PAGE_SIZE + r) * kKvd + 8 * g;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) ka[pg][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep all loads ahead of the math
 
   // Block-diagonal query tile as the B operand, hi + lo: lane (g, r) holds
   // head r's query (times 1/8) at dims [32 ks + 8 g, +8) of the KV row when
@@ -124,7 +161,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   for (int ks = 0; ks < 4; ++ks) {
     const int d0 = 32 * ks + 8 * g;
     const int kvh = d0 / 64;
-    const bool mine = ks < ks_count && r < n_heads && r / group == kvh;
+    const bool mine = r < n_heads && r / group == kvh;
     float x[8];
     if (mine) {
       const float4* src =
@@ -145,116 +182,98 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     }
   }
 
-  // 1. S^T per page: lane (g, r) gets tokens 4g..4g+3 of the page for head r.
+  // 2. S^T per page (lane (g, r): tokens 4g..4g+3 of the page, head r), then the
+  //    wave's own softmax statistics (base 2); waves are merged at the end.
   f32x4 s[4];
 #pragma unroll
-  for (int pg = 0; pg < 4; ++pg) {
-    s[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (page_ok[pg]) {
-      const uint16_t* krow = k_pool + (size_t(page[pg]) * IE_HIP_PAGE_SIZE + r) * kv_dim + 8 * g;
-      op ka[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        if (ks < ks_count) ka[ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (ks < ks_count) {
-          s[pg] = M::mma(ka[ks], qhi[ks], s[pg]);
-          s[pg] = M::mma(ka[ks], qlo[ks], s[pg]);
-        }
-      }
-    }
-  }
-
-  // 2. Softmax statistics per head (base 2).
-  float mloc = -INFINITY;
-#pragma unroll
-  for (int pg = 0; pg < 4; ++pg)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = wt0 + 16 * pg + 4 * g + i;
-      const float v = (page_ok[pg] && tok < n) ? s[pg][i] * kLog2e : -INFINITY;
-      s[pg][i] = v;
-      mloc = fmaxf(mloc, v);
-    }
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-  if (g == 0) red_m[wave * 16 + r] = mloc;
-  __syncthreads();
-  float m2 = -INFINITY;
-  for (int w = 0; w < waves; ++w) m2 = fmaxf(m2, red_m[w * 16 + r]);
-
-  op phi[2], plo[2];  // A operands of the two page pairs
-  float lsum = 0.0f;
-#pragma unroll
-  for (int pg = 0; pg < 4; ++pg)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float e = exp2f(s[pg][i] - m2);  // masked: exp2(-inf) = 0
-      lsum += e;
-      const E hi = static_cast<E>(e);
-      phi[pg >> 1][(pg & 1) * 4 + i] = hi;
-      plo[pg >> 1][(pg & 1) * 4 + i] = static_cast<E>(e - static_cast<float>(hi));
-    }
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-  if (g == 0) red_l[wave * 16 + r] = lsum;
-
-  // 3. O += P V, one page pair at a time through this wave's LDS tile.
-  E* vt = vtile_all + size_t(wave) * kVTileHalfs;
+  for (int pg = 0; pg < 4; ++pg) s[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mw = -INFINITY, lw = 0.0f;
   f32x4 o[8];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int row_chunks = kv_dim / 8;  // 16-byte pieces per KV row
+  if (active) {
 #pragma unroll
-  for (int pp = 0; pp < 2; ++pp) {
-    if (pp) __syncthreads();  // every lane has read the previous pair's tile
-    // stage: 32 rows x kv_dim, lane-contiguous 16-byte pieces
-    for (int id = lane; id < 32 * row_chunks; id += 64) {
-      const int tok = id / row_chunks, piece = id % row_chunks;
-      const int pg = 2 * pp + tok / 16;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (page_ok[pg])
-        val = *reinterpret_cast<const uint4*>(
-            v_pool + (size_t(page[pg]) * IE_HIP_PAGE_SIZE + tok % 16) * kv_dim + 8 * piece);
-      uint2* dst = reinterpret_cast<uint2*>(vt + tok * kVStride + 8 * piece);
-      dst[0] = make_uint2(val.x, val.y);
-      dst[1] = make_uint2(val.z, val.w);
-    }
-    __syncthreads();
-    // B operand slot j of lane group g holds pair token 4g+j (j<4) or 16+4g+j-4.
+    for (int pg = 0; pg < 4; ++pg)
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      if (nt * 16 < kv_dim) {
+      for (int ks = 0; ks < 4; ++ks) {
+        s[pg] = M::mma(ka[pg][ks], qhi[ks], s[pg]);
+        s[pg] = M::mma(ka[pg][ks], qlo[ks], s[pg]);
+      }
+#pragma unroll
+    for (int pg = 0; pg < 4; ++pg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = wt0 + 16 * pg + 4 * g + i;
+        const float v = (page_ok[pg] && tok < n) ? s[pg][i] * kLog2e : -INFINITY;
+        s[pg][i] = v;
+        mw = fmaxf(mw, v);
+      }
+    mw = fmaxf(mw, __shfl_xor(mw, 16, 64));
+    mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
+    op phi[2], plo[2];  // A operands of the two page pairs
+#pragma unroll
+    for (int pg = 0; pg < 4; ++pg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = exp2f(s[pg][i] - mw);  // masked: exp2(-inf) = 0
+        lw += e;
+        const E hi = static_cast<E>(e);
+        phi[pg >> 1][(pg & 1) * 4 + i] = hi;
+        plo[pg >> 1][(pg & 1) * 4 + i] = static_cast<E>(e - static_cast<float>(hi));
+      }
+    lw += __shfl_xor(lw, 16, 64);
+    lw += __shfl_xor(lw, 32, 64);
+
+    // 3. O += P V: B operand slot j of lane group g holds pair token 4g+j (j < 4)
+    //    or 16+4g+j-4, dim 16 nt + r, read from the swizzled tile.
+    __builtin_amdgcn_s_waitcnt(0);  // the LDS DMA of V has landed
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const E* vt = reinterpret_cast<const E*>(warea + pp * 8192);
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
         op b;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int tok = (j < 4) ? (4 * g + j) : (16 + 4 * g + j - 4);
-          b[j] = vt[tok * kVStride + 16 * nt + r];
+          const int slot = (2 * nt + (r >> 3)) ^ (2 * ((tok >> 2) & 3));
+          b[j] = vt[tok * 128 + slot * 8 + (r & 7)];
         }
         o[nt] = M::mma(phi[pp], b, o[nt]);
         o[nt] = M::mma(plo[pp], b, o[nt]);
       }
     }
   }
-  __syncthreads();  // V tiles are free: reuse them for the O tiles
 
-  // 4. Per-wave O tiles -> LDS [wave][16 heads][kv_dim] floats, then summed.
-  float* ot = reinterpret_cast<float*>(vtile_all) + size_t(wave) * 16 * kKvd;
+  // 4. Per-wave O tile [16 heads][128] floats into the wave's own area (its V
+  //    reads are done), per-wave (m, l); then waves are merged for the diagonal
+  //    blocks (head h, its KV head's 64 dims).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  float* ot = reinterpret_cast<float*>(warea);
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt)
-    if (nt * 16 < kv_dim)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ot[(4 * g + i) * kKvd + 16 * nt + r] = o[nt][i];
+    for (int i = 0; i < 4; ++i) ot[(4 * g + i) * kKvd + 16 * nt + r] = o[nt][i];
+  if (g == 0) {
+    red_m[wave * 16 + r] = mw;
+    red_l[wave * 16 + r] = lw;
+  }
   __syncthreads();
-  const float* ot_all = reinterpret_cast<const float*>(vtile_all);
   for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
     const int h = idx >> 6, d = idx & 63;
     const int col = (h / group) * 64 + d;
+    float mx = -INFINITY;
+    for (int w = 0; w < waves; ++w) mx = fmaxf(mx, red_m[w * 16 + h]);
     float acc = 0.0f, l = 0.0f;
     for (int w = 0; w < waves; ++w) {
-      acc += ot_all[(size_t(w) * 16 + h) * kKvd + col];
-      l += red_l[w * 16 + h];
+      const float mwh = red_m[w * 16 + h];
+      if (mwh == -INFINITY) continue;  // a wave with no positions
+      const float sc = exp2f(mwh - mx);
+      acc = __builtin_fmaf(reinterpret_cast<const float*>(smem + size_t(w) * kWaveLds)[h * kKvd + col],
+                           sc, acc);
+      l = __builtin_fmaf(red_l[w * 16 + h], sc, l);
     }
     const size_t head = size_t(t) * n_heads + h;
     if (chunks_row == 1) {
@@ -263,13 +282,41 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
       const size_t slot = head * num_chunks + c;
       part_o[slot * 64 + d] = acc;
       if (d == 0) {
-        float mm = -INFINITY;
-        for (int w = 0; w < waves; ++w) mm = fmaxf(mm, red_m[w * 16 + h]);
-        part_ml[2 * slot] = mm * kLn2;  // natural-log units, as the merge expects
+        part_ml[2 * slot] = mx * kLn2;  // natural-log units
         part_ml[2 * slot + 1] = l;
       }
     }
   }
+  if (chunks_row == 1) return;
+
+  // 5. Merge, fused: the last chunk of the row to finish combines all chunks
+  //    (M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L) and
+  //    resets the row's counter for the next launch. Release/acquire at device
+  //    scope makes the other chunks' partials (written from other XCDs) visible.
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const int done = __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_ACQ_REL,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    s_last = done == chunks_row - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
+    const int h = idx >> 6, d = idx & 63;
+    const size_t base = (size_t(t) * n_heads + h) * num_chunks;
+    float mx = -INFINITY;
+    for (int cc = 0; cc < chunks_row; ++cc) mx = fmaxf(mx, part_ml[2 * (base + cc)]);
+    float L = 0.0f, acc = 0.0f;
+    for (int cc = 0; cc < chunks_row; ++cc) {
+      const float w = expf(part_ml[2 * (base + cc)] - mx);
+      L = __builtin_fmaf(part_ml[2 * (base + cc) + 1], w, L);
+      acc = __builtin_fmaf(part_o[(base + cc) * 64 + d], w, acc);
+    }
+    out[(size_t(t) * n_heads + h) * 64 + d] = acc / L;
+  }
+  if (tid == 0) __hip_atomic_store(counters + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -277,7 +324,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
 bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim,
                            int chunk_tokens) {
   return (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) && head_dim == 64 &&
-         n_kv_heads >= 1 && n_kv_heads * head_dim <= kKvd && n_heads <= 16 &&
+         n_kv_heads * head_dim == kKvd && n_heads <= 16 &&
          n_heads % n_kv_heads == 0 && chunk_tokens % 64 == 0 && chunk_tokens >= 64 &&
          chunk_tokens <= 512;
 }
@@ -288,13 +335,12 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
                 hipStream_t stream) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
   const int waves = chunk_tokens / 64;
-  const int kv_dim = n_kv_heads * 64;
-  const size_t lds = size_t(waves) * kVTileHalfs * 2 + size_t(waves) * 16 * 2 * sizeof(float);
+  const size_t lds = size_t(waves) * (kWaveLds + 16 * 2 * sizeof(float));
   const dim3 grid(T, num_chunks), block(64 * waves);
   const int group = n_heads / n_kv_heads;
   const uint16_t* kp = static_cast<const uint16_t*>(k_pool);
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
-  // 8 waves need ~69 KB of LDS: above the 64 KB default cap for dynamic LDS,
+  // 8 waves need 129 KB of LDS: above the 64 KB default cap for dynamic LDS,
   // within gfx950's 160 KB per workgroup. Raise the cap once per kernel.
   static const hipError_t attr_f16 = hipFuncSetAttribute(
       reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_F16>),
@@ -307,14 +353,13 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
     return rc;
   if (kv.kv_dtype == IE_KV_F16)
     hipLaunchKernelGGL(decode_partial_mfma<IE_KV_F16>, grid, block, lds, stream, out, ws.part_o,
-                       ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, kv.max_pages,
-                       kv.num_pages, n_heads, group, kv_dim, num_chunks, chunk_tokens);
+                       ws.part_ml, ws.counters, q, kp, vp, row_pos, row_seq, kv.tables,
+                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens);
   else
     hipLaunchKernelGGL(decode_partial_mfma<IE_KV_BF16>, grid, block, lds, stream, out, ws.part_o,
-                       ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, kv.max_pages,
-                       kv.num_pages, n_heads, group, kv_dim, num_chunks, chunk_tokens);
-  if (int rc = check_launch("attention_partial_mfma")) return rc;
-  return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
+                       ws.part_ml, ws.counters, q, kp, vp, row_pos, row_seq, kv.tables,
+                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens);
+  return check_launch("attention_mfma");
 }
 
 }  // namespace iehip
