@@ -36,6 +36,8 @@
 //      writes `out` directly, otherwise the chunk writes (o, m, l) and the last
 //      chunk of the row to finish merges them (atomic counter per row in the
 //      workspace, reset by that chunk): one launch, no separate merge kernel.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "decode.hpp"
 
@@ -48,6 +50,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKvd = 128;                 // elements per KV row (n_kv_heads * 64)
 constexpr int kWaveLds = 16384;           // per-wave LDS: two 8 KB V page-pair tiles
+// How chunk partials are combined.
+constexpr int kMergeKernel = 0;    // a separate merge kernel
+constexpr int kMergeFence = 1;     // fused: last chunk merges; device-scope fences
+constexpr int kMergeCoherent = 2;  // fused: last chunk merges; device-coherent stores/loads
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxLds = 8 * (kWaveLds + 16 * 2 * 4);  // 8 waves
@@ -81,7 +87,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
                     const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ row_pos,
                     const int32_t* __restrict__ row_seq, const int32_t* __restrict__ tables,
                     int max_pages, int num_pages, int n_heads, int group, int num_chunks,
-                    int chunk_tokens) {
+                    int chunk_tokens, int merge_mode) {
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
@@ -280,39 +286,65 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
       out[head * 64 + d] = acc / l;
     } else {
       const size_t slot = head * num_chunks + c;
-      part_o[slot * 64 + d] = acc;
-      if (d == 0) {
-        part_ml[2 * slot] = mx * kLn2;  // natural-log units
-        part_ml[2 * slot + 1] = l;
+      if (merge_mode == kMergeCoherent) {  // written through to the device coherence point
+        __hip_atomic_store(part_o + slot * 64 + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+          __hip_atomic_store(part_ml + 2 * slot, mx * kLn2, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(part_ml + 2 * slot + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        part_o[slot * 64 + d] = acc;
+        if (d == 0) {
+          part_ml[2 * slot] = mx * kLn2;  // natural-log units
+          part_ml[2 * slot + 1] = l;
+        }
       }
     }
   }
-  if (chunks_row == 1) return;
+  if (chunks_row == 1 || merge_mode == kMergeKernel) return;
 
   // 5. Merge, fused: the last chunk of the row to finish combines all chunks
   //    (M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L) and
-  //    resets the row's counter for the next launch. Release/acquire at device
-  //    scope makes the other chunks' partials (written from other XCDs) visible.
-  __threadfence();
+  //    resets the row's counter for the next launch.
+  //    kMergeFence: release/acquire fences at device scope (these write back and
+  //      invalidate the XCD's whole L2).
+  //    kMergeCoherent: partials are stored and loaded with device-scope relaxed
+  //      atomics (coherent at the device level, no L2 flush); the stores are
+  //      waited for before the counter is bumped, and the merging workgroup only
+  //      loads them after it has seen the final count.
+  if (merge_mode == kMergeFence) {
+    __threadfence();
+  } else {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are complete
+  }
   __syncthreads();
   if (tid == 0) {
-    const int done = __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_ACQ_REL,
-                                            __HIP_MEMORY_SCOPE_AGENT);
+    const int done = merge_mode == kMergeFence
+                         ? __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_ACQ_REL,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                         : __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
     s_last = done == chunks_row - 1;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
+  if (merge_mode == kMergeFence) __threadfence();
   for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
     const int h = idx >> 6, d = idx & 63;
     const size_t base = (size_t(t) * n_heads + h) * num_chunks;
+    auto ld = [&](const float* ptr) {
+      return merge_mode == kMergeFence
+                 ? *ptr
+                 : __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     float mx = -INFINITY;
-    for (int cc = 0; cc < chunks_row; ++cc) mx = fmaxf(mx, part_ml[2 * (base + cc)]);
+    for (int cc = 0; cc < chunks_row; ++cc) mx = fmaxf(mx, ld(part_ml + 2 * (base + cc)));
     float L = 0.0f, acc = 0.0f;
     for (int cc = 0; cc < chunks_row; ++cc) {
-      const float w = expf(part_ml[2 * (base + cc)] - mx);
-      L = __builtin_fmaf(part_ml[2 * (base + cc) + 1], w, L);
-      acc = __builtin_fmaf(part_o[(base + cc) * 64 + d], w, acc);
+      const float w = expf(ld(part_ml + 2 * (base + cc)) - mx);
+      L = __builtin_fmaf(ld(part_ml + 2 * (base + cc) + 1), w, L);
+      acc = __builtin_fmaf(ld(part_o + (base + cc) * 64 + d), w, acc);
     }
     out[(size_t(t) * n_heads + h) * 64 + d] = acc / L;
   }
@@ -337,6 +369,10 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
   const int waves = chunk_tokens / 64;
   const size_t lds = size_t(waves) * (kWaveLds + 16 * 2 * sizeof(float));
   const dim3 grid(T, num_chunks), block(64 * waves);
+  static const int mode = [] {
+    const char* e = getenv("IE_HIP_DECODE_MERGE");
+    return e ? atoi(e) : kMergeKernel;
+  }();
   const int group = n_heads / n_kv_heads;
   const uint16_t* kp = static_cast<const uint16_t*>(k_pool);
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
@@ -354,12 +390,17 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
   if (kv.kv_dtype == IE_KV_F16)
     hipLaunchKernelGGL(decode_partial_mfma<IE_KV_F16>, grid, block, lds, stream, out, ws.part_o,
                        ws.part_ml, ws.counters, q, kp, vp, row_pos, row_seq, kv.tables,
-                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens);
+                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens,
+                       mode);
   else
     hipLaunchKernelGGL(decode_partial_mfma<IE_KV_BF16>, grid, block, lds, stream, out, ws.part_o,
                        ws.part_ml, ws.counters, q, kp, vp, row_pos, row_seq, kv.tables,
-                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens);
-  return check_launch("attention_mfma");
+                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens,
+                       mode);
+  if (int rc = check_launch("attention_mfma")) return rc;
+  if (mode == kMergeKernel)
+    return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
+  return IE_HIP_OK;
 }
 
 }  // namespace iehip
