@@ -49,14 +49,17 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKvd = 128;                 // elements per KV row (n_kv_heads * 64)
-constexpr int kWaveLds = 16384;           // per-wave LDS: two 8 KB V page-pair tiles
+constexpr int kWaveTokens = 128;          // positions per wave: 8 pages = 4 page pairs
+constexpr int kWavePages = kWaveTokens / IE_HIP_PAGE_SIZE;
+constexpr int kWaveLds = 8192;            // per-wave LDS: one V page-pair tile, then the O tile
 // How chunk partials are combined.
 constexpr int kMergeKernel = 0;    // a separate merge kernel
 constexpr int kMergeFence = 1;     // fused: last chunk merges; device-scope fences
 constexpr int kMergeCoherent = 2;  // fused: last chunk merges; device-coherent stores/loads
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kMaxLds = 8 * (kWaveLds + 16 * 2 * 4);  // 8 waves
+constexpr int kMaxWaves = 4;
+constexpr int kMaxLds = kMaxWaves * (kWaveLds + 16 * 2 * 4);
 
 template <int KV>
 struct Mfma;
@@ -79,8 +82,37 @@ struct Mfma<IE_KV_BF16> {
   }
 };
 
+// Wave-local pieces of the kernel, one page pair (32 positions) at a time.
 template <int KV>
-__global__ void __launch_bounds__(512)
+struct PairIo {
+  using op = typename Mfma<KV>::op;
+  op k[2][4];   // K of the pair's two pages, A-operand layout
+  uint4 v[8];   // V of the pair in coalesced 16-byte pieces
+};
+
+// Issues the loads of one page pair (pages p0, p1) into `io`.
+template <int KV>
+__device__ __forceinline__ void load_pair(PairIo<KV>& io, const uint16_t* __restrict__ k_pool,
+                                          const uint16_t* __restrict__ v_pool, int p0, int p1,
+                                          int lane) {
+  using op = typename Mfma<KV>::op;
+  const int g = lane >> 4, r = lane & 15;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int tok = 4 * u + (lane >> 4), piece = lane & 15;  // 0..31 within the pair
+    io.v[u] = *reinterpret_cast<const uint4*>(
+        v_pool + (size_t(tok < 16 ? p0 : p1) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint16_t* krow = k_pool + (size_t(h ? p1 : p0) * IE_HIP_PAGE_SIZE + r) * kKvd + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) io.k[h][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
+  }
+}
+
+template <int KV>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
                     float* __restrict__ part_ml, int32_t* __restrict__ counters,
                     const float* __restrict__ q, const uint16_t* __restrict__ k_pool,
@@ -94,8 +126,6 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_last;
   const int waves = blockDim.x >> 6;
-  // LDS: per wave a 16 KB V area (two 8 KB page-pair tiles, later the O tile),
-  // then per-wave head maxima and sums.
   float* red_m = reinterpret_cast<float*>(smem + size_t(waves) * kWaveLds);
   float* red_l = red_m + waves * 16;
 
@@ -108,56 +138,38 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   const int seq = row_seq[t];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
-  const int wt0 = wave * 64;      // first position of this wave within the chunk
-  const bool active = wt0 < n;    // wave-uniform: the wave has positions to read
-  unsigned char* warea = smem + size_t(wave) * kWaveLds;
+  const int wt0 = wave * kWaveTokens;  // first position of this wave within the chunk
+  const int wn = min(max(n - wt0, 0), kWaveTokens);  // this wave's positions
+  const int npairs = (wn + 31) / 32;                  // wave-uniform
+  E* vt = reinterpret_cast<E*>(smem + size_t(wave) * kWaveLds);
 
-  // Page ids of this wave's 4 pages. A page past the context or outside the
-  // pool is replaced by the wave's first page (re-read from cache, masked).
-  int page[4];
-  bool page_ok[4];
+  // Page ids of this wave's pages; a page past the context or outside the pool
+  // is replaced by the wave's first page (read again from cache, then masked).
+  int page[kWavePages];
+  bool page_ok[kWavePages];
+  {
+    const int32_t* row_tab = tables + size_t(seq) * max_pages;
+    int first_page = 0;
 #pragma unroll
-  for (int pg = 0; pg < 4; ++pg) {
-    const int first = wt0 + 16 * pg;
-    const int pi = (s0 + first) / IE_HIP_PAGE_SIZE;
-    int id = -1;
-    if (first < n && pi < max_pages) id = tables[size_t(seq) * max_pages + pi];
-    page_ok[pg] = id >= 0 && id < num_pages;
-    page[pg] = id;
-  }
-#pragma unroll
-  for (int pg = 0; pg < 4; ++pg)
-    if (!page_ok[pg]) page[pg] = page_ok[0] ? page[0] : 0;
-
-  // 1. Every load of the wave is issued before any math (one memory round trip):
-  //    V straight into LDS by DMA (global_load_lds_dwordx4: lane l of a load lands
-  //    at base + 16 l), K into the MFMA A-operand registers (lane (g, r): token r
-  //    of the page, 16-byte slice g of each 64-byte quarter row).
-  //    V tile of a page pair: 32 rows of 256 bytes, 16-byte piece k of row `tok`
-  //    stored at slot k ^ 2*((tok >> 2) & 3), so the transposed reads below hit
-  //    four different bank groups for the four lane groups.
-  op ka[4][4];
-  if (active) {
-#pragma unroll
-    for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int tok = 4 * u + (lane >> 4);                    // 0..31 within the pair
-        const int piece = (lane & 15) ^ (2 * (u & 3));          // global piece for slot lane&15
-        const uint16_t* src = v_pool +
-            (size_t(page[2 * pp + (tok >> 4)]) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece;
-        __builtin_amdgcn_global_load_lds(
-            (const void __attribute__((address_space(1)))*)(src),
-            (void __attribute__((address_space(3)))*)(warea + pp * 8192 + u * 1024), 16, 0, 0);
-      }
-#pragma unroll
-    for (int pg = 0; pg < 4; ++pg) {
-      const uint16_t* krow = k_pool + (size_t(page[pg]) * IE_HIP_PAGE_SIZE + r) * kKvd + 8 * g;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) ka[pg][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
+    for (int pg = 0; pg < kWavePages; ++pg) {
+      const int first = wt0 + 16 * pg;
+      const int pi = (s0 + first) / IE_HIP_PAGE_SIZE;
+      int id = -1;
+      if (first < n && pi < max_pages) id = row_tab[pi];
+      page_ok[pg] = id >= 0 && id < num_pages;
+      page[pg] = id;
+      if (pg == 0 && page_ok[0]) first_page = id;
     }
+#pragma unroll
+    for (int pg = 0; pg < kWavePages; ++pg)
+      if (!page_ok[pg]) page[pg] = first_page;
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep all loads ahead of the math
+
+  // Two page pairs in flight from the start; each later pair is requested as
+  // soon as the registers of the pair two steps back are free.
+  PairIo<KV> io[2];
+  if (npairs > 0) load_pair<KV>(io[0], k_pool, v_pool, page[0], page[1], lane);
+  if (npairs > 1) load_pair<KV>(io[1], k_pool, v_pool, page[2], page[3], lane);
 
   // Block-diagonal query tile as the B operand, hi + lo: lane (g, r) holds
   // head r's query (times 1/8) at dims [32 ks + 8 g, +8) of the KV row when
@@ -188,55 +200,82 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     }
   }
 
-  // 2. S^T per page (lane (g, r): tokens 4g..4g+3 of the page, head r), then the
-  //    wave's own softmax statistics (base 2); waves are merged at the end.
-  f32x4 s[4];
-#pragma unroll
-  for (int pg = 0; pg < 4; ++pg) s[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float mw = -INFINITY, lw = 0.0f;
+  // Online softmax over the wave's pairs: running max m (base 2), sum l, O.
+  float m_run = -INFINITY, l_run = 0.0f;
   f32x4 o[8];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (active) {
-#pragma unroll
-    for (int pg = 0; pg < 4; ++pg)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        s[pg] = M::mma(ka[pg][ks], qhi[ks], s[pg]);
-        s[pg] = M::mma(ka[pg][ks], qlo[ks], s[pg]);
-      }
-#pragma unroll
-    for (int pg = 0; pg < 4; ++pg)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = wt0 + 16 * pg + 4 * g + i;
-        const float v = (page_ok[pg] && tok < n) ? s[pg][i] * kLog2e : -INFINITY;
-        s[pg][i] = v;
-        mw = fmaxf(mw, v);
-      }
-    mw = fmaxf(mw, __shfl_xor(mw, 16, 64));
-    mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
-    op phi[2], plo[2];  // A operands of the two page pairs
-#pragma unroll
-    for (int pg = 0; pg < 4; ++pg)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = exp2f(s[pg][i] - mw);  // masked: exp2(-inf) = 0
-        lw += e;
-        const E hi = static_cast<E>(e);
-        phi[pg >> 1][(pg & 1) * 4 + i] = hi;
-        plo[pg >> 1][(pg & 1) * 4 + i] = static_cast<E>(e - static_cast<float>(hi));
-      }
-    lw += __shfl_xor(lw, 16, 64);
-    lw += __shfl_xor(lw, 32, 64);
 
-    // 3. O += P V: B operand slot j of lane group g holds pair token 4g+j (j < 4)
-    //    or 16+4g+j-4, dim 16 nt + r, read from the swizzled tile.
-    __builtin_amdgcn_s_waitcnt(0);  // the LDS DMA of V has landed
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
-      const E* vt = reinterpret_cast<const E*>(warea + pp * 8192);
+  for (int pp = 0; pp < kWavePages / 2; ++pp) {
+    if (pp < npairs) {
+      PairIo<KV>& cur = io[pp & 1];
+      // S^T of the pair's two pages: lane (g, r) gets tokens 4g..4g+3, head r.
+      f32x4 s[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          s[h] = M::mma(cur.k[h][ks], qhi[ks], s[h]);
+          s[h] = M::mma(cur.k[h][ks], qlo[ks], s[h]);
+        }
+      }
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int pg = 2 * pp + h;
+          const int tok = wt0 + 16 * pg + 4 * g + i;
+          const float v = (page_ok[pg] && tok < n) ? s[h][i] * kLog2e : -INFINITY;
+          s[h][i] = v;
+          mloc = fmaxf(mloc, v);
+        }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m_run, mloc);
+      // rows of O belong to heads 4g+i: fetch their rescale factors from lane 4g+i
+      const float corr = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
+      m_run = m_new;
+      op phi, plo;
+      float lsum = 0.0f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = m_new == -INFINITY ? 0.0f : exp2f(s[h][i] - m_new);
+          lsum += e;
+          const E hi = static_cast<E>(e);
+          phi[4 * h + i] = hi;
+          plo[4 * h + i] = static_cast<E>(e - static_cast<float>(hi));
+        }
+      lsum += __shfl_xor(lsum, 16, 64);
+      lsum += __shfl_xor(lsum, 32, 64);
+      l_run = l_run * corr + lsum;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ci = __shfl(corr, 4 * g + i, 64);
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) o[nt][i] *= ci;
+      }
+      // V of the pair through the wave's LDS tile (swizzled: 16-byte piece k of
+      // row `tok` at slot k ^ 2*((tok >> 2) & 3)), read back transposed.
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int tok = 4 * u + (lane >> 4), piece = lane & 15;
+        const int slot = piece ^ (2 * ((tok >> 2) & 3));
+        *reinterpret_cast<uint4*>(vt + tok * kKvd + 8 * slot) = cur.v[u];
+      }
+      // the pair two steps ahead may now reuse these registers
+      if (pp + 2 < npairs) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_pair<KV>(cur, k_pool, v_pool, page[2 * pp + 4], page[2 * pp + 5], lane);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
         op b;
@@ -244,27 +283,28 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
         for (int j = 0; j < 8; ++j) {
           const int tok = (j < 4) ? (4 * g + j) : (16 + 4 * g + j - 4);
           const int slot = (2 * nt + (r >> 3)) ^ (2 * ((tok >> 2) & 3));
-          b[j] = vt[tok * 128 + slot * 8 + (r & 7)];
+          b[j] = vt[tok * kKvd + slot * 8 + (r & 7)];
         }
-        o[nt] = M::mma(phi[pp], b, o[nt]);
-        o[nt] = M::mma(plo[pp], b, o[nt]);
+        o[nt] = M::mma(phi, b, o[nt]);
+        o[nt] = M::mma(plo, b, o[nt]);
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 
-  // 4. Per-wave O tile [16 heads][128] floats into the wave's own area (its V
-  //    reads are done), per-wave (m, l); then waves are merged for the diagonal
-  //    blocks (head h, its KV head's 64 dims).
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  float* ot = reinterpret_cast<float*>(warea);
+  // Per-wave O tile [16 heads][128] floats into the wave's own LDS area, per-wave
+  // (m, l); then the waves are merged for the diagonal blocks (head h, its KV
+  // head's 64 dims).
+  float* ot = reinterpret_cast<float*>(smem + size_t(wave) * kWaveLds);
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) ot[(4 * g + i) * kKvd + 16 * nt + r] = o[nt][i];
   if (g == 0) {
-    red_m[wave * 16 + r] = mw;
-    red_l[wave * 16 + r] = lw;
+    red_m[wave * 16 + r] = m_run;
+    red_l[wave * 16 + r] = l_run;
   }
   __syncthreads();
   for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
@@ -357,8 +397,8 @@ bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_d
                            int chunk_tokens) {
   return (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) && head_dim == 64 &&
          n_kv_heads * head_dim == kKvd && n_heads <= 16 &&
-         n_heads % n_kv_heads == 0 && chunk_tokens % 64 == 0 && chunk_tokens >= 64 &&
-         chunk_tokens <= 512;
+         n_heads % n_kv_heads == 0 && chunk_tokens % kWaveTokens == 0 &&
+         chunk_tokens >= kWaveTokens && chunk_tokens <= kMaxWaves * kWaveTokens;
 }
 
 int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
@@ -366,7 +406,7 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
                 hipStream_t stream) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
-  const int waves = chunk_tokens / 64;
+  const int waves = chunk_tokens / kWaveTokens;
   const size_t lds = size_t(waves) * (kWaveLds + 16 * 2 * sizeof(float));
   const dim3 grid(T, num_chunks), block(64 * waves);
   static const int mode = [] {
@@ -376,8 +416,7 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
   const int group = n_heads / n_kv_heads;
   const uint16_t* kp = static_cast<const uint16_t*>(k_pool);
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
-  // 8 waves need 129 KB of LDS: above the 64 KB default cap for dynamic LDS,
-  // within gfx950's 160 KB per workgroup. Raise the cap once per kernel.
+  // Keep the dynamic-LDS cap explicit (4 waves use 33 KB).
   static const hipError_t attr_f16 = hipFuncSetAttribute(
       reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_F16>),
       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
