@@ -210,25 +210,46 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
   }
 }
 
-// One workgroup per (head, row), one thread per output dim.
+// One workgroup per (head, row), one thread per output dim. The partials of up
+// to 32 chunks are loaded together (independent loads, one memory round trip),
+// then combined: M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L.
+// Longer rows take further batches with the running (M, L, acc) rescaled.
 template <int HD>
 __global__ void __launch_bounds__(HD)
 decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
                     const float* __restrict__ part_ml, const int32_t* __restrict__ row_pos,
                     int n_heads, int num_chunks, int chunk_tokens) {
+  constexpr int kBatch = 32;
   const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
   const int p = row_pos[t];
   if (p < 0) return;
   const int nc = min(p / chunk_tokens + 1, num_chunks);
   if (nc <= 1) return;  // written by the partial kernel
   const size_t base = (size_t(t) * n_heads + h) * num_chunks;
-  float M = -INFINITY;
-  for (int c = 0; c < nc; ++c) M = fmaxf(M, part_ml[2 * (base + c)]);
-  float L = 0.0f, acc = 0.0f;
-  for (int c = 0; c < nc; ++c) {
-    const float w = expf(part_ml[2 * (base + c)] - M);
-    L = __builtin_fmaf(part_ml[2 * (base + c) + 1], w, L);
-    acc = __builtin_fmaf(part_o[(base + c) * HD + d], w, acc);
+  const float2* ml = reinterpret_cast<const float2*>(part_ml) + base;
+  float M = -INFINITY, L = 0.0f, acc = 0.0f;
+  for (int c0 = 0; c0 < nc; c0 += kBatch) {
+    float2 mlc[kBatch];
+    float oc[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const bool ok = c0 + j < nc;
+      mlc[j] = ok ? ml[c0 + j] : make_float2(-INFINITY, 0.0f);
+      oc[j] = ok ? part_o[(base + c0 + j) * HD + d] : 0.0f;
+    }
+    float mb = M;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, mlc[j].x);
+    const float sc = M == -INFINITY ? 0.0f : expf(M - mb);
+    L *= sc;
+    acc *= sc;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const float w = c0 + j < nc ? expf(mlc[j].x - mb) : 0.0f;
+      L = __builtin_fmaf(mlc[j].y, w, L);
+      acc = __builtin_fmaf(oc[j], w, acc);
+    }
+    M = mb;
   }
   out[(size_t(t) * n_heads + h) * HD + d] = acc / L;
 }

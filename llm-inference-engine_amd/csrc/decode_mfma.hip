@@ -21,8 +21,12 @@
 // 2^-22 |x|), each product done twice: float32-level scores and weights.
 //
 // Layout of the work:
-//   grid (T, num_chunks), rows fastest; chunk_tokens / 64 (<= 8) waves per workgroup,
-//   each wave owns 64 consecutive positions = 4 pages = 2 page pairs.
+//   grid (T, num_chunks), rows fastest; chunk_tokens / 64 waves per workgroup
+//   (2 at the default 128-token chunk), each wave owns 64 consecutive
+//   positions = 4 pages = 2 page pairs. A workgroup takes exactly 16 KB of LDS
+//   per wave and ~136 VGPRs per lane, so 5 two-wave workgroups fit on a CU and a
+//   whole batch-64 decode step is resident at once (one round of workgroups,
+//   every load of the step in flight from the start).
 //   1. All K and V loads of the wave are issued first (one memory round trip).
 //      K goes straight into the MFMA A-operand registers (4 x 16-byte loads per
 //      page; lanes 0-15 hold tokens 0-15, the 4 lane groups hold the 4 16-byte
@@ -32,12 +36,12 @@
 //   3. V: each page pair (8 KB) is staged in a per-wave LDS tile with 16-byte
 //      coalesced loads and read back transposed (one 2-byte element per lane per
 //      slot) as the B operand; 16 MFMA 16x16x32 per pair.
-//   4. O: per-wave tiles summed through LDS; a row whose context fits one chunk
-//      writes `out` directly, otherwise the chunk writes (o, m, l) and the last
-//      chunk of the row to finish merges them (atomic counter per row in the
-//      workspace, reset by that chunk): one launch, no separate merge kernel.
-#include <cstdlib>
-
+//   4. O: per-wave tiles merged through LDS (log-sum-exp across the waves); a row
+//      whose context fits one chunk writes `out` directly, otherwise the chunk
+//      writes (o, m, l) and decode_merge_kernel (decode.hip) combines the chunks.
+//      Merging inside this kernel instead (last chunk of a row, atomic counter)
+//      was measured slower on MI355X: device-scope fences write back and
+//      invalidate the XCD's L2, and the per-row counter serialises the chunks.
 #include "common.hpp"
 #include "decode.hpp"
 
@@ -49,17 +53,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKvd = 128;                 // elements per KV row (n_kv_heads * 64)
-constexpr int kWaveTokens = 128;          // positions per wave: 8 pages = 4 page pairs
-constexpr int kWavePages = kWaveTokens / IE_HIP_PAGE_SIZE;
-constexpr int kWaveLds = 8192;            // per-wave LDS: one V page-pair tile, then the O tile
-// How chunk partials are combined.
-constexpr int kMergeKernel = 0;    // a separate merge kernel
-constexpr int kMergeFence = 1;     // fused: last chunk merges; device-scope fences
-constexpr int kMergeCoherent = 2;  // fused: last chunk merges; device-coherent stores/loads
+constexpr int kWaveLds = 16384;           // per-wave LDS: two 8 KB V page-pair tiles;
+                                          // later the O tile (8 KB) and the wave's (m, l)
+constexpr int kMaxWaves = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kMaxWaves = 4;
-constexpr int kMaxLds = kMaxWaves * (kWaveLds + 16 * 2 * 4);
+constexpr int kMaxLds = kMaxWaves * kWaveLds;
 
 template <int KV>
 struct Mfma;
@@ -82,52 +81,22 @@ struct Mfma<IE_KV_BF16> {
   }
 };
 
-// Wave-local pieces of the kernel, one page pair (32 positions) at a time.
 template <int KV>
-struct PairIo {
-  using op = typename Mfma<KV>::op;
-  op k[2][4];   // K of the pair's two pages, A-operand layout
-  uint4 v[8];   // V of the pair in coalesced 16-byte pieces
-};
-
-// Issues the loads of one page pair (pages p0, p1) into `io`.
-template <int KV>
-__device__ __forceinline__ void load_pair(PairIo<KV>& io, const uint16_t* __restrict__ k_pool,
-                                          const uint16_t* __restrict__ v_pool, int p0, int p1,
-                                          int lane) {
-  using op = typename Mfma<KV>::op;
-  const int g = lane >> 4, r = lane & 15;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int tok = 4 * u + (lane >> 4), piece = lane & 15;  // 0..31 within the pair
-    io.v[u] = *reinterpret_cast<const uint4*>(
-        v_pool + (size_t(tok < 16 ? p0 : p1) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece);
-  }
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint16_t* krow = k_pool + (size_t(h ? p1 : p0) * IE_HIP_PAGE_SIZE + r) * kKvd + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) io.k[h][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
-  }
-}
-
-template <int KV>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(512)
 decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
-                    float* __restrict__ part_ml, int32_t* __restrict__ counters,
-                    const float* __restrict__ q, const uint16_t* __restrict__ k_pool,
-                    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ row_pos,
-                    const int32_t* __restrict__ row_seq, const int32_t* __restrict__ tables,
-                    int max_pages, int num_pages, int n_heads, int group, int num_chunks,
-                    int chunk_tokens, int merge_mode) {
+                    float* __restrict__ part_ml, const float* __restrict__ q,
+                    const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
+                    const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
+                    const int32_t* __restrict__ tables, int max_pages, int num_pages, int n_heads,
+                    int group, int num_chunks, int chunk_tokens) {
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_last;
   const int waves = blockDim.x >> 6;
-  float* red_m = reinterpret_cast<float*>(smem + size_t(waves) * kWaveLds);
-  float* red_l = red_m + waves * 16;
+  // per-wave head maxima / sums live after the wave's O tile
+  auto red_m = [&](int w) { return reinterpret_cast<float*>(smem + size_t(w) * kWaveLds + 8192); };
+  auto red_l = [&](int w) { return red_m(w) + 16; };
 
   const int t = blockIdx.x, c = blockIdx.y;
   const int p = row_pos[t];
@@ -138,38 +107,56 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   const int seq = row_seq[t];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
-  const int wt0 = wave * kWaveTokens;  // first position of this wave within the chunk
-  const int wn = min(max(n - wt0, 0), kWaveTokens);  // this wave's positions
-  const int npairs = (wn + 31) / 32;                  // wave-uniform
-  E* vt = reinterpret_cast<E*>(smem + size_t(wave) * kWaveLds);
+  const int wt0 = wave * 64;      // first position of this wave within the chunk
+  const bool active = wt0 < n;    // wave-uniform: the wave has positions to read
+  unsigned char* warea = smem + size_t(wave) * kWaveLds;
 
-  // Page ids of this wave's pages; a page past the context or outside the pool
-  // is replaced by the wave's first page (read again from cache, then masked).
-  int page[kWavePages];
-  bool page_ok[kWavePages];
-  {
-    const int32_t* row_tab = tables + size_t(seq) * max_pages;
-    int first_page = 0;
+  // Page ids of this wave's 4 pages. A page past the context or outside the
+  // pool is replaced by the wave's first page (re-read from cache, masked).
+  int page[4];
+  bool page_ok[4];
 #pragma unroll
-    for (int pg = 0; pg < kWavePages; ++pg) {
-      const int first = wt0 + 16 * pg;
-      const int pi = (s0 + first) / IE_HIP_PAGE_SIZE;
-      int id = -1;
-      if (first < n && pi < max_pages) id = row_tab[pi];
-      page_ok[pg] = id >= 0 && id < num_pages;
-      page[pg] = id;
-      if (pg == 0 && page_ok[0]) first_page = id;
-    }
-#pragma unroll
-    for (int pg = 0; pg < kWavePages; ++pg)
-      if (!page_ok[pg]) page[pg] = first_page;
+  for (int pg = 0; pg < 4; ++pg) {
+    const int first = wt0 + 16 * pg;
+    const int pi = (s0 + first) / IE_HIP_PAGE_SIZE;
+    int id = -1;
+    if (first < n && pi < max_pages) id = tables[size_t(seq) * max_pages + pi];
+    page_ok[pg] = id >= 0 && id < num_pages;
+    page[pg] = id;
   }
+#pragma unroll
+  for (int pg = 0; pg < 4; ++pg)
+    if (!page_ok[pg]) page[pg] = page_ok[0] ? page[0] : 0;
 
-  // Two page pairs in flight from the start; each later pair is requested as
-  // soon as the registers of the pair two steps back are free.
-  PairIo<KV> io[2];
-  if (npairs > 0) load_pair<KV>(io[0], k_pool, v_pool, page[0], page[1], lane);
-  if (npairs > 1) load_pair<KV>(io[1], k_pool, v_pool, page[2], page[3], lane);
+  // 1. Every load of the wave is issued before any math (one memory round trip):
+  //    V straight into LDS by DMA (global_load_lds_dwordx4: lane l of a load lands
+  //    at base + 16 l), K into the MFMA A-operand registers (lane (g, r): token r
+  //    of the page, 16-byte slice g of each 64-byte quarter row).
+  //    V tile of a page pair: 32 rows of 256 bytes, 16-byte piece k of row `tok`
+  //    stored at slot k ^ 2*((tok >> 2) & 3), so the transposed reads below hit
+  //    four different bank groups for the four lane groups.
+  op ka[4][4];
+  if (active) {
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int tok = 4 * u + (lane >> 4);                    // 0..31 within the pair
+        const int piece = (lane & 15) ^ (2 * (u & 3));          // global piece for slot lane&15
+        const uint16_t* src = v_pool +
+            (size_t(page[2 * pp + (tok >> 4)]) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece;
+        __builtin_amdgcn_global_load_lds(
+            (const void __attribute__((address_space(1)))*)(src),
+            (void __attribute__((address_space(3)))*)(warea + pp * 8192 + u * 1024), 16, 0, 0);
+      }
+#pragma unroll
+    for (int pg = 0; pg < 4; ++pg) {
+      const uint16_t* krow = k_pool + (size_t(page[pg]) * IE_HIP_PAGE_SIZE + r) * kKvd + 8 * g;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) ka[pg][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep all loads ahead of the math
 
   // Block-diagonal query tile as the B operand, hi + lo: lane (g, r) holds
   // head r's query (times 1/8) at dims [32 ks + 8 g, +8) of the KV row when
@@ -200,82 +187,55 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     }
   }
 
-  // Online softmax over the wave's pairs: running max m (base 2), sum l, O.
-  float m_run = -INFINITY, l_run = 0.0f;
+  // 2. S^T per page (lane (g, r): tokens 4g..4g+3 of the page, head r), then the
+  //    wave's own softmax statistics (base 2); waves are merged at the end.
+  f32x4 s[4];
+#pragma unroll
+  for (int pg = 0; pg < 4; ++pg) s[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mw = -INFINITY, lw = 0.0f;
   f32x4 o[8];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
+  if (active) {
 #pragma unroll
-  for (int pp = 0; pp < kWavePages / 2; ++pp) {
-    if (pp < npairs) {
-      PairIo<KV>& cur = io[pp & 1];
-      // S^T of the pair's two pages: lane (g, r) gets tokens 4g..4g+3, head r.
-      f32x4 s[2];
+    for (int pg = 0; pg < 4; ++pg)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          s[h] = M::mma(cur.k[h][ks], qhi[ks], s[h]);
-          s[h] = M::mma(cur.k[h][ks], qlo[ks], s[h]);
-        }
+      for (int ks = 0; ks < 4; ++ks) {
+        s[pg] = M::mma(ka[pg][ks], qhi[ks], s[pg]);
+        s[pg] = M::mma(ka[pg][ks], qlo[ks], s[pg]);
       }
-      float mloc = -INFINITY;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int pg = 2 * pp + h;
-          const int tok = wt0 + 16 * pg + 4 * g + i;
-          const float v = (page_ok[pg] && tok < n) ? s[h][i] * kLog2e : -INFINITY;
-          s[h][i] = v;
-          mloc = fmaxf(mloc, v);
-        }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m_run, mloc);
-      // rows of O belong to heads 4g+i: fetch their rescale factors from lane 4g+i
-      const float corr = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
-      m_run = m_new;
-      op phi, plo;
-      float lsum = 0.0f;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = m_new == -INFINITY ? 0.0f : exp2f(s[h][i] - m_new);
-          lsum += e;
-          const E hi = static_cast<E>(e);
-          phi[4 * h + i] = hi;
-          plo[4 * h + i] = static_cast<E>(e - static_cast<float>(hi));
-        }
-      lsum += __shfl_xor(lsum, 16, 64);
-      lsum += __shfl_xor(lsum, 32, 64);
-      l_run = l_run * corr + lsum;
+    for (int pg = 0; pg < 4; ++pg)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float ci = __shfl(corr, 4 * g + i, 64);
+        const int tok = wt0 + 16 * pg + 4 * g + i;
+        const float v = (page_ok[pg] && tok < n) ? s[pg][i] * kLog2e : -INFINITY;
+        s[pg][i] = v;
+        mw = fmaxf(mw, v);
+      }
+    mw = fmaxf(mw, __shfl_xor(mw, 16, 64));
+    mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
+    op phi[2], plo[2];  // A operands of the two page pairs
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) o[nt][i] *= ci;
-      }
-      // V of the pair through the wave's LDS tile (swizzled: 16-byte piece k of
-      // row `tok` at slot k ^ 2*((tok >> 2) & 3)), read back transposed.
+    for (int pg = 0; pg < 4; ++pg)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int tok = 4 * u + (lane >> 4), piece = lane & 15;
-        const int slot = piece ^ (2 * ((tok >> 2) & 3));
-        *reinterpret_cast<uint4*>(vt + tok * kKvd + 8 * slot) = cur.v[u];
+      for (int i = 0; i < 4; ++i) {
+        const float e = exp2f(s[pg][i] - mw);  // masked: exp2(-inf) = 0
+        lw += e;
+        const E hi = static_cast<E>(e);
+        phi[pg >> 1][(pg & 1) * 4 + i] = hi;
+        plo[pg >> 1][(pg & 1) * 4 + i] = static_cast<E>(e - static_cast<float>(hi));
       }
-      // the pair two steps ahead may now reuse these registers
-      if (pp + 2 < npairs) {
-        __builtin_amdgcn_sched_barrier(0);
-        load_pair<KV>(cur, k_pool, v_pool, page[2 * pp + 4], page[2 * pp + 5], lane);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    lw += __shfl_xor(lw, 16, 64);
+    lw += __shfl_xor(lw, 32, 64);
+
+    // 3. O += P V: B operand slot j of lane group g holds pair token 4g+j (j < 4)
+    //    or 16+4g+j-4, dim 16 nt + r, read from the swizzled tile.
+    __builtin_amdgcn_s_waitcnt(0);  // the LDS DMA of V has landed
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const E* vt = reinterpret_cast<const E*>(warea + pp * 8192);
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
         op b;
@@ -283,112 +243,55 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
         for (int j = 0; j < 8; ++j) {
           const int tok = (j < 4) ? (4 * g + j) : (16 + 4 * g + j - 4);
           const int slot = (2 * nt + (r >> 3)) ^ (2 * ((tok >> 2) & 3));
-          b[j] = vt[tok * kKvd + slot * 8 + (r & 7)];
+          b[j] = vt[tok * 128 + slot * 8 + (r & 7)];
         }
-        o[nt] = M::mma(phi, b, o[nt]);
-        o[nt] = M::mma(plo, b, o[nt]);
+        o[nt] = M::mma(phi[pp], b, o[nt]);
+        o[nt] = M::mma(plo[pp], b, o[nt]);
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 
-  // Per-wave O tile [16 heads][128] floats into the wave's own LDS area, per-wave
-  // (m, l); then the waves are merged for the diagonal blocks (head h, its KV
-  // head's 64 dims).
-  float* ot = reinterpret_cast<float*>(smem + size_t(wave) * kWaveLds);
+  // 4. Per-wave O tile [16 heads][128] floats into the wave's own area (its V
+  //    reads are done), per-wave (m, l); then waves are merged for the diagonal
+  //    blocks (head h, its KV head's 64 dims).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  float* ot = reinterpret_cast<float*>(warea);
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) ot[(4 * g + i) * kKvd + 16 * nt + r] = o[nt][i];
   if (g == 0) {
-    red_m[wave * 16 + r] = m_run;
-    red_l[wave * 16 + r] = l_run;
+    red_m(wave)[r] = mw;
+    red_l(wave)[r] = lw;
   }
   __syncthreads();
   for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
     const int h = idx >> 6, d = idx & 63;
     const int col = (h / group) * 64 + d;
     float mx = -INFINITY;
-    for (int w = 0; w < waves; ++w) mx = fmaxf(mx, red_m[w * 16 + h]);
+    for (int w = 0; w < waves; ++w) mx = fmaxf(mx, red_m(w)[h]);
     float acc = 0.0f, l = 0.0f;
     for (int w = 0; w < waves; ++w) {
-      const float mwh = red_m[w * 16 + h];
+      const float mwh = red_m(w)[h];
       if (mwh == -INFINITY) continue;  // a wave with no positions
       const float sc = exp2f(mwh - mx);
       acc = __builtin_fmaf(reinterpret_cast<const float*>(smem + size_t(w) * kWaveLds)[h * kKvd + col],
                            sc, acc);
-      l = __builtin_fmaf(red_l[w * 16 + h], sc, l);
+      l = __builtin_fmaf(red_l(w)[h], sc, l);
     }
     const size_t head = size_t(t) * n_heads + h;
     if (chunks_row == 1) {
       out[head * 64 + d] = acc / l;
     } else {
       const size_t slot = head * num_chunks + c;
-      if (merge_mode == kMergeCoherent) {  // written through to the device coherence point
-        __hip_atomic_store(part_o + slot * 64 + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (d == 0) {
-          __hip_atomic_store(part_ml + 2 * slot, mx * kLn2, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(part_ml + 2 * slot + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      } else {
-        part_o[slot * 64 + d] = acc;
-        if (d == 0) {
-          part_ml[2 * slot] = mx * kLn2;  // natural-log units
-          part_ml[2 * slot + 1] = l;
-        }
+      part_o[slot * 64 + d] = acc;
+      if (d == 0) {
+        part_ml[2 * slot] = mx * kLn2;  // natural-log units
+        part_ml[2 * slot + 1] = l;
       }
     }
   }
-  if (chunks_row == 1 || merge_mode == kMergeKernel) return;
-
-  // 5. Merge, fused: the last chunk of the row to finish combines all chunks
-  //    (M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L) and
-  //    resets the row's counter for the next launch.
-  //    kMergeFence: release/acquire fences at device scope (these write back and
-  //      invalidate the XCD's whole L2).
-  //    kMergeCoherent: partials are stored and loaded with device-scope relaxed
-  //      atomics (coherent at the device level, no L2 flush); the stores are
-  //      waited for before the counter is bumped, and the merging workgroup only
-  //      loads them after it has seen the final count.
-  if (merge_mode == kMergeFence) {
-    __threadfence();
-  } else {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are complete
-  }
-  __syncthreads();
-  if (tid == 0) {
-    const int done = merge_mode == kMergeFence
-                         ? __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_ACQ_REL,
-                                                  __HIP_MEMORY_SCOPE_AGENT)
-                         : __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-    s_last = done == chunks_row - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  if (merge_mode == kMergeFence) __threadfence();
-  for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
-    const int h = idx >> 6, d = idx & 63;
-    const size_t base = (size_t(t) * n_heads + h) * num_chunks;
-    auto ld = [&](const float* ptr) {
-      return merge_mode == kMergeFence
-                 ? *ptr
-                 : __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-    float mx = -INFINITY;
-    for (int cc = 0; cc < chunks_row; ++cc) mx = fmaxf(mx, ld(part_ml + 2 * (base + cc)));
-    float L = 0.0f, acc = 0.0f;
-    for (int cc = 0; cc < chunks_row; ++cc) {
-      const float w = expf(ld(part_ml + 2 * (base + cc)) - mx);
-      L = __builtin_fmaf(ld(part_ml + 2 * (base + cc) + 1), w, L);
-      acc = __builtin_fmaf(ld(part_o + (base + cc) * 64 + d), w, acc);
-    }
-    out[(size_t(t) * n_heads + h) * 64 + d] = acc / L;
-  }
-  if (tid == 0) __hip_atomic_store(counters + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -397,8 +300,8 @@ bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_d
                            int chunk_tokens) {
   return (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) && head_dim == 64 &&
          n_kv_heads * head_dim == kKvd && n_heads <= 16 &&
-         n_heads % n_kv_heads == 0 && chunk_tokens % kWaveTokens == 0 &&
-         chunk_tokens >= kWaveTokens && chunk_tokens <= kMaxWaves * kWaveTokens;
+         n_heads % n_kv_heads == 0 && chunk_tokens % 64 == 0 && chunk_tokens >= 64 &&
+         chunk_tokens <= 512;
 }
 
 int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
@@ -406,17 +309,14 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
                 hipStream_t stream) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
-  const int waves = chunk_tokens / kWaveTokens;
-  const size_t lds = size_t(waves) * (kWaveLds + 16 * 2 * sizeof(float));
+  const int waves = chunk_tokens / 64;
+  const size_t lds = size_t(waves) * kWaveLds;
   const dim3 grid(T, num_chunks), block(64 * waves);
-  static const int mode = [] {
-    const char* e = getenv("IE_HIP_DECODE_MERGE");
-    return e ? atoi(e) : kMergeKernel;
-  }();
   const int group = n_heads / n_kv_heads;
   const uint16_t* kp = static_cast<const uint16_t*>(k_pool);
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
-  // Keep the dynamic-LDS cap explicit (4 waves use 33 KB).
+  // 8 waves (512-token chunks) need 128 KB of LDS: above the 64 KB default cap
+  // for dynamic LDS, within gfx950's 160 KB per workgroup. Raise it once.
   static const hipError_t attr_f16 = hipFuncSetAttribute(
       reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_F16>),
       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
@@ -428,18 +328,14 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
     return rc;
   if (kv.kv_dtype == IE_KV_F16)
     hipLaunchKernelGGL(decode_partial_mfma<IE_KV_F16>, grid, block, lds, stream, out, ws.part_o,
-                       ws.part_ml, ws.counters, q, kp, vp, row_pos, row_seq, kv.tables,
-                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens,
-                       mode);
+                       ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, kv.max_pages,
+                       kv.num_pages, n_heads, group, num_chunks, chunk_tokens);
   else
     hipLaunchKernelGGL(decode_partial_mfma<IE_KV_BF16>, grid, block, lds, stream, out, ws.part_o,
-                       ws.part_ml, ws.counters, q, kp, vp, row_pos, row_seq, kv.tables,
-                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens,
-                       mode);
+                       ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, kv.max_pages,
+                       kv.num_pages, n_heads, group, num_chunks, chunk_tokens);
   if (int rc = check_launch("attention_mfma")) return rc;
-  if (mode == kMergeKernel)
-    return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
-  return IE_HIP_OK;
+  return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
 }
 
 }  // namespace iehip
