@@ -94,17 +94,21 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   using E = typename M::elem;
   extern __shared__ __align__(16) unsigned char smem[];
   const int waves = blockDim.x >> 6;
-  // per-wave head maxima / sums live after the wave's O tile
+  // LDS per wave (16 KB): two 8 KB V page-pair tiles; after the PV products the
+  // first 8 KB hold the wave's O tile [16 heads][128] and the next bytes its
+  // per-head (m, l). Wave 0's area also holds the per-(wave, head) merge scales.
   auto red_m = [&](int w) { return reinterpret_cast<float*>(smem + size_t(w) * kWaveLds + 8192); };
   auto red_l = [&](int w) { return red_m(w) + 16; };
+  float* comb_sc = reinterpret_cast<float*>(smem + 8192 + 256);  // [kMaxWaves][16]
+  float* comb_il = comb_sc + kMaxWaves * 16;                       // [16] 1 / L
 
   const int t = blockIdx.x, c = blockIdx.y;
   const int p = row_pos[t];
+  const int seq = row_seq[t];
   const int s0 = c * chunk_tokens;
   if (p < 0 || s0 > p) return;  // future chunk: the whole workgroup leaves
   const int n = min(s0 + chunk_tokens, p + 1) - s0;
-  const int chunks_row = min(p / chunk_tokens + 1, num_chunks);
-  const int seq = row_seq[t];
+  const bool single = s0 == 0 && p < chunk_tokens;  // the row fits this one chunk
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
   const int wt0 = wave * 64;      // first position of this wave within the chunk
@@ -115,34 +119,36 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   // pool is replaced by the wave's first page (re-read from cache, masked).
   int page[4];
   bool page_ok[4];
+  {
+    const int32_t* row_tab = tables + size_t(seq) * max_pages + (s0 + wt0) / IE_HIP_PAGE_SIZE;
+    const int pi0 = (s0 + wt0) / IE_HIP_PAGE_SIZE;
 #pragma unroll
-  for (int pg = 0; pg < 4; ++pg) {
-    const int first = wt0 + 16 * pg;
-    const int pi = (s0 + first) / IE_HIP_PAGE_SIZE;
-    int id = -1;
-    if (first < n && pi < max_pages) id = tables[size_t(seq) * max_pages + pi];
-    page_ok[pg] = id >= 0 && id < num_pages;
-    page[pg] = id;
+    for (int pg = 0; pg < 4; ++pg) {
+      int id = -1;
+      if (wt0 + 16 * pg < n && pi0 + pg < max_pages) id = row_tab[pg];
+      page_ok[pg] = id >= 0 && id < num_pages;
+      page[pg] = id;
+    }
+#pragma unroll
+    for (int pg = 0; pg < 4; ++pg)
+      if (!page_ok[pg]) page[pg] = page_ok[0] ? page[0] : 0;
   }
-#pragma unroll
-  for (int pg = 0; pg < 4; ++pg)
-    if (!page_ok[pg]) page[pg] = page_ok[0] ? page[0] : 0;
 
   // 1. Every load of the wave is issued before any math (one memory round trip):
   //    V straight into LDS by DMA (global_load_lds_dwordx4: lane l of a load lands
   //    at base + 16 l), K into the MFMA A-operand registers (lane (g, r): token r
   //    of the page, 16-byte slice g of each 64-byte quarter row).
-  //    V tile of a page pair: 32 rows of 256 bytes, 16-byte piece k of row `tok`
-  //    stored at slot k ^ 2*((tok >> 2) & 3), so the transposed reads below hit
-  //    four different bank groups for the four lane groups.
+  //    V tile of a page pair: 32 rows of 256 bytes; 16-byte piece k of row `tok`
+  //    is stored at slot k ^ 2*(tok & 7), so that the transposed reads below (8
+  //    rows x 32 bytes per half-wave) fall into distinct banks.
   op ka[4][4];
   if (active) {
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int tok = 4 * u + (lane >> 4);                    // 0..31 within the pair
-        const int piece = (lane & 15) ^ (2 * (u & 3));          // global piece for slot lane&15
+        const int tok = 4 * u + g;                           // 0..31 within the pair
+        const int piece = r ^ (2 * (tok & 7));               // global piece for slot r
         const uint16_t* src = v_pool +
             (size_t(page[2 * pp + (tok >> 4)]) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece;
         __builtin_amdgcn_global_load_lds(
@@ -160,50 +166,47 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
 
   // Block-diagonal query tile as the B operand, hi + lo: lane (g, r) holds
   // head r's query (times 1/8) at dims [32 ks + 8 g, +8) of the KV row when
-  // those dims belong to head r's KV head, zeros otherwise.
+  // those dims belong to head r's KV head (ks / 2), zeros otherwise.
   op qhi[4], qlo[4];
+  {
+    const int r_kvh = r >= group;  // kv head of query head r (two KV heads)
+    const float* qrow = q + (size_t(t) * n_heads + r) * 64 + 8 * g;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int d0 = 32 * ks + 8 * g;
-    const int kvh = d0 / 64;
-    const bool mine = r < n_heads && r / group == kvh;
-    float x[8];
-    if (mine) {
-      const float4* src =
-          reinterpret_cast<const float4*>(q + (size_t(t) * n_heads + r) * 64 + (d0 - 64 * kvh));
-      const float4 a = src[0], b = src[1];
-      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-      x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-    } else {
+    for (int ks = 0; ks < 4; ++ks) {
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+      if (r < n_heads && r_kvh == (ks >> 1)) {
+        const float4* src = reinterpret_cast<const float4*>(qrow + 32 * (ks & 1));
+        a = src[0];
+        b = src[1];
+      }
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float v = x[j] * 0.125f;
-      const E hi = static_cast<E>(v);
-      qhi[ks][j] = hi;
-      qlo[ks][j] = static_cast<E>(v - static_cast<float>(hi));
+      for (int j = 0; j < 8; ++j) {
+        const float v = x[j] * 0.125f;
+        const E hi = static_cast<E>(v);
+        qhi[ks][j] = hi;
+        qlo[ks][j] = static_cast<E>(v - static_cast<float>(hi));
+      }
     }
   }
 
   // 2. S^T per page (lane (g, r): tokens 4g..4g+3 of the page, head r), then the
   //    wave's own softmax statistics (base 2); waves are merged at the end.
-  f32x4 s[4];
-#pragma unroll
-  for (int pg = 0; pg < 4; ++pg) s[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
   float mw = -INFINITY, lw = 0.0f;
   f32x4 o[8];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (active) {
+    f32x4 s[4];
 #pragma unroll
-    for (int pg = 0; pg < 4; ++pg)
+    for (int pg = 0; pg < 4; ++pg) {
+      s[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         s[pg] = M::mma(ka[pg][ks], qhi[ks], s[pg]);
         s[pg] = M::mma(ka[pg][ks], qlo[ks], s[pg]);
       }
+    }
 #pragma unroll
     for (int pg = 0; pg < 4; ++pg)
 #pragma unroll
@@ -229,21 +232,34 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     lw += __shfl_xor(lw, 16, 64);
     lw += __shfl_xor(lw, 32, 64);
 
-    // 3. O += P V: B operand slot j of lane group g holds pair token 4g+j (j < 4)
-    //    or 16+4g+j-4, dim 16 nt + r, read from the swizzled tile.
+    // 3. O += P V. The B operand (pair token 4g+j in slot j < 4, 16+4g+j-4 in
+    //    slot j >= 4; dim 16 nt + r) comes from two transposing LDS reads
+    //    (ds_read_b64_tr_b16): in each 16-lane group, lane 4a+b receives element
+    //    b of the 8-byte reads of lanes a, a+4, a+8, a+12; lane L reads row
+    //    4g + L/4, dims 16 nt + 4 (L%4) .. +3, so lane r receives dim 16 nt + r of
+    //    rows 4g..4g+3 (and 16+4g.. for the second read).
     __builtin_amdgcn_s_waitcnt(0);  // the LDS DMA of V has landed
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const int rtok = 4 * g + (r >> 2);  // row this lane reads (first read)
+    const int rsw = rtok & 7;           // its swizzle key
+    const int rlo = (r & 1) * 8;        // byte within the 16-byte piece
+    const int rpc = (r >> 1) & 1;       // piece parity within the 32-byte unit
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
-      const E* vt = reinterpret_cast<const E*>(warea + pp * 8192);
+      const unsigned char* vt = warea + pp * 8192 + rtok * 256 + rlo;
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
+        const int slot = 2 * (nt ^ rsw) + rpc;
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        const s4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s4*)(vt + slot * 16));
+        const s4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s4*)(vt + 16 * 256 + slot * 16));
         op b;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int tok = (j < 4) ? (4 * g + j) : (16 + 4 * g + j - 4);
-          const int slot = (2 * nt + (r >> 3)) ^ (2 * ((tok >> 2) & 3));
-          b[j] = vt[tok * 128 + slot * 8 + (r & 7)];
+        for (int j = 0; j < 4; ++j) {
+          b[j] = __builtin_bit_cast(E, lo4[j]);
+          b[4 + j] = __builtin_bit_cast(E, hi4[j]);
         }
         o[nt] = M::mma(phi[pp], b, o[nt]);
         o[nt] = M::mma(plo[pp], b, o[nt]);
@@ -252,8 +268,8 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   }
 
   // 4. Per-wave O tile [16 heads][128] floats into the wave's own area (its V
-  //    reads are done), per-wave (m, l); then waves are merged for the diagonal
-  //    blocks (head h, its KV head's 64 dims).
+  //    reads are done) and per-wave (m, l); then the waves are merged
+  //    (log-sum-exp) for the diagonal blocks (head h, its KV head's 64 dims).
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   float* ot = reinterpret_cast<float*>(warea);
@@ -266,30 +282,44 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     red_l(wave)[r] = lw;
   }
   __syncthreads();
-  for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
-    const int h = idx >> 6, d = idx & 63;
-    const int col = (h / group) * 64 + d;
+  if (tid < n_heads) {  // per head: chunk max, merge scale of each wave, sum, 1 / sum
+    const int h = tid;
     float mx = -INFINITY;
     for (int w = 0; w < waves; ++w) mx = fmaxf(mx, red_m(w)[h]);
-    float acc = 0.0f, l = 0.0f;
+    float l = 0.0f;
     for (int w = 0; w < waves; ++w) {
       const float mwh = red_m(w)[h];
-      if (mwh == -INFINITY) continue;  // a wave with no positions
-      const float sc = exp2f(mwh - mx);
-      acc = __builtin_fmaf(reinterpret_cast<const float*>(smem + size_t(w) * kWaveLds)[h * kKvd + col],
-                           sc, acc);
+      const float sc = mwh == -INFINITY ? 0.0f : exp2f(mwh - mx);
+      comb_sc[w * 16 + h] = sc;
       l = __builtin_fmaf(red_l(w)[h], sc, l);
     }
-    const size_t head = size_t(t) * n_heads + h;
-    if (chunks_row == 1) {
-      out[head * 64 + d] = acc / l;
-    } else {
-      const size_t slot = head * num_chunks + c;
-      part_o[slot * 64 + d] = acc;
-      if (d == 0) {
-        part_ml[2 * slot] = mx * kLn2;  // natural-log units
-        part_ml[2 * slot + 1] = l;
-      }
+    comb_il[h] = 1.0f / l;
+    if (!single) {
+      const size_t slot = (size_t(t) * n_heads + h) * num_chunks + c;
+      part_ml[2 * slot] = mx * kLn2;  // natural-log units
+      part_ml[2 * slot + 1] = l;
+    }
+  }
+  __syncthreads();
+  // Each thread owns outputs idx = tid + k * blockDim (head idx / 64, dim idx % 64).
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int idx = tid + k * int(blockDim.x);
+    if (idx < n_heads * 64) {
+      const int h = idx >> 6, d = idx & 63;
+      const int col = (h >= group ? 64 : 0) + d;
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kMaxWaves; ++w)
+        if (w < waves)
+          acc = __builtin_fmaf(
+              reinterpret_cast<const float*>(smem + size_t(w) * kWaveLds)[h * kKvd + col],
+              comb_sc[w * 16 + h], acc);
+      const size_t head = size_t(t) * n_heads + h;
+      if (single)
+        out[head * 64 + d] = acc * comb_il[h];
+      else
+        part_o[(head * num_chunks + c) * 64 + d] = acc;
     }
   }
 }
