@@ -302,10 +302,9 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   }
   __syncthreads();
   // Each thread owns outputs idx = tid + k * blockDim (head idx / 64, dim idx % 64).
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int idx = tid + k * int(blockDim.x);
-    if (idx < n_heads * 64) {
+#pragma unroll 4
+  for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
+    {
       const int h = idx >> 6, d = idx & 63;
       const int col = (h >= group ? 64 : 0) + d;
       float acc = 0.0f;
