@@ -51,6 +51,7 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKvd = 128;                 // elements per KV row (n_kv_heads * 64)
 constexpr int kWaveLds = 16384;           // per-wave LDS: two 8 KB V page-pair tiles;
@@ -250,17 +251,13 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
         const int slot = 2 * (nt ^ rsw) + rpc;
-        typedef short s4 __attribute__((ext_vector_type(4)));
         const s4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s4*)(vt + slot * 16));
         const s4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s4*)(vt + 16 * 256 + slot * 16));
-        op b;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          b[j] = __builtin_bit_cast(E, lo4[j]);
-          b[4 + j] = __builtin_bit_cast(E, hi4[j]);
-        }
+        // Joined as whole vectors: element-wise extraction of these results
+        // miscompiles (it broadcasts element 0) with this toolchain.
+        const op b = __builtin_bit_cast(op, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
         o[nt] = M::mma(phi[pp], b, o[nt]);
         o[nt] = M::mma(plo[pp], b, o[nt]);
       }
