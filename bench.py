@@ -274,6 +274,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true", help="config 2: rows-per-launch sweep")
     ap.add_argument("--probe", action="store_true", help="also measure device copy bandwidth")
+    ap.add_argument("--probe-only", action="store_true",
+                    help="only the device copy (the plain copy kernel that rocprofv3 byte "
+                         "counters are calibrated on)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this path has no multi-GPU mode (the paged KV "
@@ -290,6 +293,10 @@ def main():
     ie.set_attention_impl({"auto": ie.IMPL_AUTO, "valu": ie.IMPL_VALU, "mfma": ie.IMPL_MFMA}[args.impl])
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
+    if args.probe_only:
+        print(json.dumps({"measured_copy_gbs": copy_probe(torch), "copy_bytes": 2 << 30}),
+              flush=True)
+        return
     res = bench_decode(args, torch, ie, O) if args.config == 3 else bench_append(args, torch, ie, O)
     if args.probe:
         res["measured_copy_gbs"] = copy_probe(torch)

@@ -403,8 +403,8 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
                        workspace, n_heads, n_kv_heads, stream);
   if (impl == IE_HIP_IMPL_MFMA)
     return fail(IE_HIP_EINVAL, "attention: the MFMA kernel does not support this shape "
-                               "(16-bit KV, kv_dim <= 128, n_heads <= 16, chunk a multiple of 64 "
-                               "up to 512)");
+                               "(16-bit KV, kv_dim 128, n_heads <= 16, chunk a multiple of 64 "
+                               "up to 1024)");
   return decode_valu(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
                      workspace, n_heads, n_kv_heads, stream);
 }

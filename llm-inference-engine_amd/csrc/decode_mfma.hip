@@ -7,41 +7,56 @@
 //
 // Why MFMA for decode: every KV row is used by all 7 query heads of its group,
 // so per 16-token page the work is two dense products,
-//     S^T[16 tok x 16 heads] = K_page[16 x 128] . Qbd^T[128 x 16]
-//     O[16 heads x 128]     += P[16 heads x 32 tok] . V_pair[32 tok x 128]
+//     S^T[16 tok x 16 heads]   = K_page[16 x 128] . Qbd^T[128 x 16]
+//     O^T[128 dims x 16 heads] += V_pair^T[128 x 32 tok] . P^T[32 tok x 16 heads]
 // where Qbd is block-diagonal: head h carries its query in the 64 dims of its
-// own KV head and zeros elsewhere, so ONE 16-row tile serves all 14 heads of
+// own KV head and zeros elsewhere, so ONE 16-column tile serves all 14 heads of
 // both KV heads and each K/V row is read exactly once. On the VALU the same
 // work costs ~1,800 FMAs per position -- as much time as streaming the cache.
-// The only extra work is the off-diagonal half of O, discarded at the end.
+// The only extra work is the off-diagonal half of O^T, discarded at the end.
+// With both products in this orientation, lane (g, r) of every tile belongs to
+// head r: the scores it holds (S^T), the weights it feeds (P^T) and the output
+// it accumulates (O^T) are all head r's, so softmax statistics never move
+// between lanes except for the reductions over the 4 lane groups.
 //
 // Precision (2e-3 absolute bound for 16-bit caches): K and V enter the MFMA in
-// their stored format, exactly. Q (pre-scaled by 1/8, exact) and P are split
+// their stored format, exactly. Q (pre-scaled by log2(e)/8) and P are split
 // into hi + lo halves of the same 16-bit type (x = hi + lo, |x - hi - lo| ~
 // 2^-22 |x|), each product done twice: float32-level scores and weights.
 //
 // Layout of the work:
-//   grid (T, num_chunks), rows fastest; chunk_tokens / 64 waves per workgroup
-//   (2 at the default 128-token chunk), each wave owns 64 consecutive
-//   positions = 4 pages = 2 page pairs. A workgroup takes exactly 16 KB of LDS
-//   per wave and ~136 VGPRs per lane, so 5 two-wave workgroups fit on a CU and a
-//   whole batch-64 decode step is resident at once (one round of workgroups,
-//   every load of the step in flight from the start).
-//   1. All K and V loads of the wave are issued first (one memory round trip).
-//      K goes straight into the MFMA A-operand registers (4 x 16-byte loads per
-//      page; lanes 0-15 hold tokens 0-15, the 4 lane groups hold the 4 16-byte
-//      slices of each 64-byte quarter row). 8 MFMA 16x16x32 per page.
-//   2. softmax over the chunk: wave-local max/sum by shuffles, across waves
-//      through LDS (scores kept in registers; base-2 exponent).
-//   3. V: each page pair (8 KB) is staged in a per-wave LDS tile with 16-byte
-//      coalesced loads and read back transposed (one 2-byte element per lane per
-//      slot) as the B operand; 16 MFMA 16x16x32 per pair.
-//   4. O: per-wave tiles merged through LDS (log-sum-exp across the waves); a row
-//      whose context fits one chunk writes `out` directly, otherwise the chunk
-//      writes (o, m, l) and decode_merge_kernel (decode.hip) combines the chunks.
-//      Merging inside this kernel instead (last chunk of a row, atomic counter)
-//      was measured slower on MI355X: device-scope fences write back and
-//      invalidate the XCD's L2, and the per-row counter serialises the chunks.
+//   One workgroup per non-empty (row, chunk) pair, with one wave per 128
+//   positions of the chunk (decode_mfma_waves); each wave streams its positions
+//   as page pairs (32 tokens, 2 pages), keeping the next pair's loads in flight
+//   while it computes the current one. The 1-D grid is numbered row by row over
+//   the chunks each row actually has (a prefix sum of the rows' chunk counts,
+//   computed by every wave from row_pos), so all real work comes first in
+//   dispatch order and the slots past the batch's total exit at once: no empty
+//   workgroup holds a CU while real ones wait. A wave takes 16 KB of LDS (two V
+//   page-pair tiles, double-buffered), so a CU holds 10 waves.
+//   1. The query, then page pair 0: K straight into the MFMA A-operand
+//      registers (lanes 0-15 hold tokens 0-15, the 4 lane groups the 4 16-byte
+//      slices of each 64-byte quarter row), V into an LDS tile by DMA.
+//   2. Per page pair, as its data lands: S^T (8 MFMA 16x16x32 per page); the
+//      next pair's loads into the other K registers and LDS tile; the online
+//      softmax update (running max and sum per head, base 2); O^T += V^T P^T,
+//      V^T read back from the tile transposed (ds_read_b64_tr_b16) as the A
+//      operand (16 MFMA per pair).
+//   3. Waves of one workgroup are merged through LDS. A row whose context fits
+//      one chunk writes `out` directly; otherwise the chunk writes its partial
+//      (o, m, l) to the workspace and decode_merge_kernel (decode.hip) combines
+//      the row's chunks. Fusing that merge into this kernel (the row's last
+//      chunk to finish merges, through a per-row atomic counter and
+//      device-coherent stores and loads) was measured slower on MI355X: its
+//      tail is three dependent memory round trips (store completion, the
+//      atomic, the partials) against one launch plus one round trip.
+//   Positions past the row's context (the tail of its last page) and pages
+//   whose id lies outside the pool are masked: their scores are -inf and their
+//   V elements are zeroed before the product, so stale or non-finite memory in
+//   those rows cannot reach the output. Page pairs with no such position skip
+//   the masking.
+#include <algorithm>
+
 #include "common.hpp"
 #include "decode.hpp"
 
@@ -53,13 +68,15 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 
-constexpr int kKvd = 128;                 // elements per KV row (n_kv_heads * 64)
-constexpr int kWaveLds = 16384;           // per-wave LDS: two 8 KB V page-pair tiles;
-                                          // later the O tile (8 KB) and the wave's (m, l)
+constexpr int kKvd = 128;          // elements per KV row (n_kv_heads * 64)
+constexpr int kPair = 8192;        // one V page-pair tile [32 tok][256 B]
+constexpr int kTile = 2 * kPair;   // per-wave LDS: the two page-pair tiles; after the
+                                   // products, the wave's output tile [16][64] f32
 constexpr int kMaxWaves = 8;
+constexpr int kOutTile = 16 * 64 * 4;        // a wave's output tile [16 heads][64] f32
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kMaxLds = kMaxWaves * kWaveLds;
+constexpr int kMaxLds = kMaxWaves * kTile;
 
 template <int KV>
 struct Mfma;
@@ -82,240 +99,340 @@ struct Mfma<IE_KV_BF16> {
   }
 };
 
-template <int KV>
-__global__ void __launch_bounds__(512)
+// s_waitcnt with only the vector-memory counter set (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt and lgkmcnt left at their "no wait" maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off, 64);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+// Workgroup `wg` -> (row t, chunk c, position p, sequence seq) in the order
+// "row 0's chunks, row 1's chunks, ...", where row t has min(p / chunk + 1,
+// num_chunks) chunks (none if p < 0). Every wave computes the same answer.
+// Returns false when wg lies past the batch's last chunk.
+__device__ __forceinline__ bool locate_chunk(int wg, int T, const int32_t* __restrict__ row_pos,
+                                             const int32_t* __restrict__ row_seq, int num_chunks,
+                                             int chunk_tokens, int lane, int& t, int& c, int& p,
+                                             int& seq) {
+  int base = 0;
+  for (int r0 = 0; r0 < T; r0 += 64) {
+    const int rr = r0 + lane;
+    const int pr = rr < T ? row_pos[rr] : -1;
+    const int sr = rr < T ? row_seq[rr] : 0;
+    const int n = pr < 0 ? 0 : min(pr / chunk_tokens + 1, num_chunks);
+    const int incl = wave_inclusive_scan(n, lane);
+    const int total = __builtin_amdgcn_readfirstlane(__shfl(incl, 63, 64));
+    if (wg < base + total) {
+      const unsigned long long m = __ballot(wg < base + incl);
+      const int L = __ffsll(m) - 1;  // first lane whose chunks reach past wg
+      t = r0 + L;
+      p = __builtin_amdgcn_readfirstlane(__shfl(pr, L, 64));
+      seq = __builtin_amdgcn_readfirstlane(__shfl(sr, L, 64));
+      c = wg - base - __builtin_amdgcn_readfirstlane(__shfl(incl - n, L, 64));
+      return true;
+    }
+    base += total;
+  }
+  return false;
+}
+
+// kOneWave: one-wave workgroups (chunks of up to 255 tokens) -- the wave's
+// softmax is the chunk's, so the epilogue writes straight from the
+// accumulators and the workgroup needs no LDS beyond its V tiles.
+template <int KV, bool kOneWave>
+__global__ void __launch_bounds__(kOneWave ? 64 : 512) __attribute__((amdgpu_waves_per_eu(3)))
 decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
                     float* __restrict__ part_ml, const float* __restrict__ q,
                     const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
                     const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
-                    const int32_t* __restrict__ tables, int max_pages, int num_pages, int n_heads,
-                    int group, int num_chunks, int chunk_tokens) {
+                    const int32_t* __restrict__ tables, int T, int max_pages, int num_pages,
+                    int n_heads, int group, int num_chunks, int chunk_tokens) {
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int waves = blockDim.x >> 6;
-  // LDS per wave (16 KB): two 8 KB V page-pair tiles; after the PV products the
-  // first 8 KB hold the wave's O tile [16 heads][128] and the next bytes its
-  // per-head (m, l). Wave 0's area also holds the per-(wave, head) merge scales.
-  auto red_m = [&](int w) { return reinterpret_cast<float*>(smem + size_t(w) * kWaveLds + 8192); };
-  auto red_l = [&](int w) { return red_m(w) + 16; };
-  float* comb_sc = reinterpret_cast<float*>(smem + 8192 + 256);  // [kMaxWaves][16]
-  float* comb_il = comb_sc + kMaxWaves * 16;                       // [16] 1 / L
-
-  const int t = blockIdx.x, c = blockIdx.y;
-  const int p = row_pos[t];
-  const int seq = row_seq[t];
-  const int s0 = c * chunk_tokens;
-  if (p < 0 || s0 > p) return;  // future chunk: the whole workgroup leaves
-  const int n = min(s0 + chunk_tokens, p + 1) - s0;
-  const bool single = s0 == 0 && p < chunk_tokens;  // the row fits this one chunk
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = kOneWave ? 0 : tid >> 6, lane = tid & 63;
   const int g = lane >> 4, r = lane & 15;
-  const int wt0 = wave * 64;      // first position of this wave within the chunk
-  const bool active = wt0 < n;    // wave-uniform: the wave has positions to read
-  unsigned char* warea = smem + size_t(wave) * kWaveLds;
+  int t, c, p, seq;
+  if (!locate_chunk(blockIdx.x, T, row_pos, row_seq, num_chunks, chunk_tokens, lane, t, c, p, seq))
+    return;  // past the batch's last chunk: the whole workgroup leaves
+  const int s0 = c * chunk_tokens;
+  const int n = min(s0 + chunk_tokens, p + 1) - s0;  // positions of this chunk
+  const bool single = s0 == 0 && p < chunk_tokens;  // the row fits this one chunk
+  const int waves = kOneWave ? 1 : blockDim.x >> 6;
+  const int tw = chunk_tokens / waves;              // positions per wave (a multiple of 32)
+  const int wt0 = wave * tw;                        // first position of this wave in the chunk
+  const int nw = min(max(n - wt0, 0), tw);          // positions this wave attends to
+  const int np = (nw + 31) >> 5;                    // its page pairs
+  unsigned char* warea = smem + size_t(wave) * kTile;
 
-  // Page ids of this wave's 4 pages. A page past the context or outside the
-  // pool is replaced by the wave's first page (re-read from cache, masked).
-  int page[4];
-  bool page_ok[4];
-  {
-    const int32_t* row_tab = tables + size_t(seq) * max_pages + (s0 + wt0) / IE_HIP_PAGE_SIZE;
-    const int pi0 = (s0 + wt0) / IE_HIP_PAGE_SIZE;
-#pragma unroll
-    for (int pg = 0; pg < 4; ++pg) {
-      int id = -1;
-      if (wt0 + 16 * pg < n && pi0 + pg < max_pages) id = row_tab[pg];
-      page_ok[pg] = id >= 0 && id < num_pages;
-      page[pg] = id;
-    }
-#pragma unroll
-    for (int pg = 0; pg < 4; ++pg)
-      if (!page_ok[pg]) page[pg] = page_ok[0] ? page[0] : 0;
+  // Page id of the wave's page `pw` (uniform, scalar load); -1 past the wave's
+  // positions or the table row.
+  const int pi0 = (s0 + wt0) / IE_HIP_PAGE_SIZE;
+  const int32_t* row_tab = tables + size_t(seq) * max_pages;
+  auto page_id = [&](const int pw) -> int {
+    const int pi = pi0 + pw;
+    return (16 * pw < nw && pi < max_pages) ? row_tab[pi] : -1;
+  };
+
+  // The query of head r (the B operand's column), dims [8g, 8g+8) and
+  // [32 + 8g, 32 + 8g + 8) of its own KV head. Loaded first, so that waiting
+  // for it does not wait for the K/V loads behind it.
+  const bool head_ok = r < n_heads;
+  const int kv_r = r >= group;  // KV head of query head r (two KV heads)
+  float4 q0a = make_float4(0.f, 0.f, 0.f, 0.f), q0b = q0a, q1a = q0a, q1b = q0a;
+  if (head_ok) {
+    const float4* qrow = reinterpret_cast<const float4*>(q + (size_t(t) * n_heads + r) * 64 + 8 * g);
+    q0a = qrow[0];
+    q0b = qrow[1];
+    q1a = qrow[8];
+    q1b = qrow[9];
   }
 
-  // 1. Every load of the wave is issued before any math (one memory round trip):
-  //    V straight into LDS by DMA (global_load_lds_dwordx4: lane l of a load lands
-  //    at base + 16 l), K into the MFMA A-operand registers (lane (g, r): token r
-  //    of the page, 16-byte slice g of each 64-byte quarter row).
-  //    V tile of a page pair: 32 rows of 256 bytes; 16-byte piece k of row `tok`
-  //    is stored at slot k ^ 2*(tok & 7), so that the transposed reads below (8
-  //    rows x 32 bytes per half-wave) fall into distinct banks.
-  op ka[4][4];
-  if (active) {
+  // Loads of page pair j (pages 2j, 2j+1 of the wave): K into the MFMA
+  // A-operand registers `ka` (lane (g, r): token r of the page, the 16-byte
+  // slice g of each 64-byte quarter row), V into LDS tile j & 1 by DMA.
+  // V tile of a page pair: 32 rows of 256 bytes; 16-byte piece k of row `tok`
+  // is stored at slot k ^ 2*(tok & 7), so that the transposed reads (8 rows x
+  // 32 bytes per half-wave) fall into distinct banks. Lane (g, r) of DMA u moves
+  // row tok = 4u + g (page u / 4 of the pair), slot r; lane l of a DMA lands at
+  // base + 16 l. A page id outside the pool (or past the context) is replaced
+  // by page 0 for the loads and masked in the math.
+  op ka[2][4];
+  auto issue = [&](const int j, const int pa, const int pb) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp)
+    for (int h = 0; h < 2; ++h) {
+      const uint16_t* krow = k_pool + (size_t(h ? pb : pa) * IE_HIP_PAGE_SIZE + r) * kKvd + 8 * g;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int tok = 4 * u + g;                           // 0..31 within the pair
-        const int piece = r ^ (2 * (tok & 7));               // global piece for slot r
-        const uint16_t* src = v_pool +
-            (size_t(page[2 * pp + (tok >> 4)]) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece;
-        __builtin_amdgcn_global_load_lds(
-            (const void __attribute__((address_space(1)))*)(src),
-            (void __attribute__((address_space(3)))*)(warea + pp * 8192 + u * 1024), 16, 0, 0);
-      }
-#pragma unroll
-    for (int pg = 0; pg < 4; ++pg) {
-      const uint16_t* krow = k_pool + (size_t(page[pg]) * IE_HIP_PAGE_SIZE + r) * kKvd + 8 * g;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) ka[pg][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
+      for (int ks = 0; ks < 4; ++ks) ka[h][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
     }
-  }
-  __builtin_amdgcn_sched_barrier(0);  // keep all loads ahead of the math
+    __builtin_amdgcn_sched_barrier(0);
+    unsigned char* tile = warea + (j & 1) * kPair;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int tok = 4 * u + g;
+      const int piece = r ^ (2 * (tok & 7));
+      const uint16_t* src = v_pool +
+          (size_t((u >> 2) ? pb : pa) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece;
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1)))*)(src),
+          (void __attribute__((address_space(3)))*)(tile + u * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto valid = [&](const int id) { return id >= 0 && id < num_pages; };
+  // Page ids of the current pair (cur_*) and of the next one (nx_*).
+  int cur_a = page_id(0), cur_b = page_id(1);
+  int nx_a = page_id(2), nx_b = page_id(3);
+  if (np > 0) issue(0, valid(cur_a) ? cur_a : 0, valid(cur_b) ? cur_b : 0);
 
-  // Block-diagonal query tile as the B operand, hi + lo: lane (g, r) holds
-  // head r's query (times 1/8) at dims [32 ks + 8 g, +8) of the KV row when
-  // those dims belong to head r's KV head (ks / 2), zeros otherwise.
+  // Query times log2(e)/8, split into hi + lo, as the B operands of the 4
+  // 32-dim steps of the 128-dim KV row: head r's values in the two steps of its
+  // own KV head, zeros in the other two.
   op qhi[4], qlo[4];
   {
-    const int r_kvh = r >= group;  // kv head of query head r (two KV heads)
-    const float* qrow = q + (size_t(t) * n_heads + r) * 64 + 8 * g;
+    const float qs = 0.125f * kLog2e;
+    const float x[2][8] = {{q0a.x, q0a.y, q0a.z, q0a.w, q0b.x, q0b.y, q0b.z, q0b.w},
+                           {q1a.x, q1a.y, q1a.z, q1a.w, q1b.x, q1b.y, q1b.z, q1b.w}};
+    op h2[2], l2[2];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-      if (r < n_heads && r_kvh == (ks >> 1)) {
-        const float4* src = reinterpret_cast<const float4*>(qrow + 32 * (ks & 1));
-        a = src[0];
-        b = src[1];
-      }
-      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    for (int k = 0; k < 2; ++k)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float v = x[j] * 0.125f;
+        const float v = x[k][j] * qs;
         const E hi = static_cast<E>(v);
-        qhi[ks][j] = hi;
-        qlo[ks][j] = static_cast<E>(v - static_cast<float>(hi));
+        h2[k][j] = hi;
+        l2[k][j] = static_cast<E>(v - static_cast<float>(hi));
       }
+    const op zero = {};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bool mine = (ks >> 1) == kv_r;
+      qhi[ks] = mine ? h2[ks & 1] : zero;
+      qlo[ks] = mine ? l2[ks & 1] : zero;
     }
   }
 
-  // 2. S^T per page (lane (g, r): tokens 4g..4g+3 of the page, head r), then the
-  //    wave's own softmax statistics (base 2); waves are merged at the end.
-  float mw = -INFINITY, lw = 0.0f;
-  f32x4 o[8];
+  // Per page pair j, as its data lands: scores, online softmax, O^T += V^T P^T,
+  // with the loads of pair j+1 issued as soon as pair j's K registers are
+  // consumed, so a wave always has one pair in flight while it computes.
+  // Lane (g, r): head r; S^T element i of the pair's page h is token
+  // 32 j + 16 h + 4g + i of the wave.
+  float m = -INFINITY, l = 0.0f;  // running max (base 2) and this lane's part of the sum
+  f32x4 o[8];                     // O^T tiles: lane (g, r) holds head r, dims 16 mt + 4g + e
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (active) {
-    f32x4 s[4];
+  for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int rtok = 4 * g + (r >> 2);  // tile row this lane reads (first of the two reads)
+  const int rsw = rtok & 7;           // its swizzle key
+  const int rlo = (r & 1) * 8;        // byte within the 16-byte piece
+  const int rpc = (r >> 1) & 1;       // piece parity within the 32-byte unit
+  for (int j = 0; j < np; ++j) {
+    // Outstanding: K and V of pair j (8 + 8 loads, in that order).
+    wait_vmcnt<8>();
+    f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
 #pragma unroll
-    for (int pg = 0; pg < 4; ++pg) {
-      s[pg] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < 4; ++ks) {
+      sa = M::mma(ka[0][ks], qhi[ks], sa);
+      sa = M::mma(ka[0][ks], qlo[ks], sa);
+      sb = M::mma(ka[1][ks], qhi[ks], sb);
+      sb = M::mma(ka[1][ks], qlo[ks], sb);
+    }
+    const bool ok_a = valid(cur_a), ok_b = valid(cur_b);
+    const bool more = j + 1 < np;
+    if (more) {  // pair j+1: K into `ka` (just consumed), V into the other tile
+      issue(j + 1, valid(nx_a) ? nx_a : 0, valid(nx_b) ? nx_b : 0);
+      cur_a = nx_a;
+      cur_b = nx_b;
+      nx_a = page_id(2 * j + 4);
+      nx_b = page_id(2 * j + 5);
+    }
+    const int tj = 32 * j;  // first token of the pair within the wave
+    const bool full = tj + 32 <= nw && ok_a && ok_b;
+    if (!full) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        s[pg] = M::mma(ka[pg][ks], qhi[ks], s[pg]);
-        s[pg] = M::mma(ka[pg][ks], qlo[ks], s[pg]);
+      for (int i = 0; i < 4; ++i) {
+        const int ta = tj + 4 * g + i, tb = ta + 16;
+        sa[i] = (ok_a && ta < nw) ? sa[i] : -INFINITY;
+        sb[i] = (ok_b && tb < nw) ? sb[i] : -INFINITY;
       }
     }
+    float mx = fmaxf(fmaxf(fmaxf(sa[0], sa[1]), fmaxf(sa[2], sa[3])),
+                     fmaxf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float mref = m_new == -INFINITY ? 0.0f : m_new;  // all masked so far: weights 0
+    op phi, plo;
+    float sum = 0.0f;
 #pragma unroll
-    for (int pg = 0; pg < 4; ++pg)
+    for (int i = 0; i < 4; ++i) {
+      const float ea = exp2f(sa[i] - mref), eb = exp2f(sb[i] - mref);
+      sum += ea + eb;
+      const E ha = static_cast<E>(ea), hb = static_cast<E>(eb);
+      phi[i] = ha;
+      phi[4 + i] = hb;
+      plo[i] = static_cast<E>(ea - static_cast<float>(ha));
+      plo[4 + i] = static_cast<E>(eb - static_cast<float>(hb));
+    }
+    if (j == 0) {
+      l = sum;
+    } else {
+      const float corr = exp2f(m - mref);  // m = -inf (nothing seen yet): 0
+      l = __builtin_fmaf(l, corr, sum);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = wt0 + 16 * pg + 4 * g + i;
-        const float v = (page_ok[pg] && tok < n) ? s[pg][i] * kLog2e : -INFINITY;
-        s[pg][i] = v;
-        mw = fmaxf(mw, v);
-      }
-    mw = fmaxf(mw, __shfl_xor(mw, 16, 64));
-    mw = fmaxf(mw, __shfl_xor(mw, 32, 64));
-    op phi[2], plo[2];  // A operands of the two page pairs
-#pragma unroll
-    for (int pg = 0; pg < 4; ++pg)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = exp2f(s[pg][i] - mw);  // masked: exp2(-inf) = 0
-        lw += e;
-        const E hi = static_cast<E>(e);
-        phi[pg >> 1][(pg & 1) * 4 + i] = hi;
-        plo[pg >> 1][(pg & 1) * 4 + i] = static_cast<E>(e - static_cast<float>(hi));
-      }
-    lw += __shfl_xor(lw, 16, 64);
-    lw += __shfl_xor(lw, 32, 64);
+      for (int mt = 0; mt < 8; ++mt) o[mt] *= corr;
+    }
+    m = m_new;
 
-    // 3. O += P V. The B operand (pair token 4g+j in slot j < 4, 16+4g+j-4 in
-    //    slot j >= 4; dim 16 nt + r) comes from two transposing LDS reads
-    //    (ds_read_b64_tr_b16): in each 16-lane group, lane 4a+b receives element
-    //    b of the 8-byte reads of lanes a, a+4, a+8, a+12; lane L reads row
-    //    4g + L/4, dims 16 nt + 4 (L%4) .. +3, so lane r receives dim 16 nt + r of
-    //    rows 4g..4g+3 (and 16+4g.. for the second read).
-    __builtin_amdgcn_s_waitcnt(0);  // the LDS DMA of V has landed
+    // V^T of the pair: two transposing reads per 16-dim tile; in each 16-lane
+    // group, lane 4a+b receives element b of the 8-byte reads of lanes a,
+    // a+4, a+8, a+12. Lane L reads tile row 4g + L/4, dims 16 mt + 4 (L%4)..+3,
+    // so lane r receives dim 16 mt + r of rows 4g..4g+3 (and 16+4g.. for the
+    // second read): the A operand, token slots matching P^T's.
+    if (more)
+      wait_vmcnt<16>();  // V of pair j has landed; pair j+1 (16 loads) may be in flight
+    else
+      wait_vmcnt<0>();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    const int rtok = 4 * g + (r >> 2);  // row this lane reads (first read)
-    const int rsw = rtok & 7;           // its swizzle key
-    const int rlo = (r & 1) * 8;        // byte within the 16-byte piece
-    const int rpc = (r >> 1) & 1;       // piece parity within the 32-byte unit
+    unsigned long long keep_lo = ~0ull, keep_hi = ~0ull;
+    if (!full) {  // 0 * (stale inf or NaN) is not 0: zero masked V elements
+      keep_lo = keep_hi = 0;
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
-      const unsigned char* vt = warea + pp * 8192 + rtok * 256 + rlo;
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        const int slot = 2 * (nt ^ rsw) + rpc;
-        const s4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s4*)(vt + slot * 16));
-        const s4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s4*)(vt + 16 * 256 + slot * 16));
-        // Joined as whole vectors: element-wise extraction of these results
-        // miscompiles (it broadcasts element 0) with this toolchain.
-        const op b = __builtin_bit_cast(op, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[nt] = M::mma(phi[pp], b, o[nt]);
-        o[nt] = M::mma(plo[pp], b, o[nt]);
+      for (int i = 0; i < 4; ++i) {
+        const int ta = tj + 4 * g + i, tb = ta + 16;
+        if (ok_a && ta < nw) keep_lo |= 0xFFFFull << (16 * i);
+        if (ok_b && tb < nw) keep_hi |= 0xFFFFull << (16 * i);
       }
     }
+    const unsigned char* vt = warea + (j & 1) * kPair + rtok * 256 + rlo;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const int slot = 2 * (mt ^ rsw) + rpc;
+      s4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s4*)(vt + slot * 16));
+      s4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s4*)(vt + 16 * 256 + slot * 16));
+      if (!full) {
+        lo4 = __builtin_bit_cast(s4, __builtin_bit_cast(unsigned long long, lo4) & keep_lo);
+        hi4 = __builtin_bit_cast(s4, __builtin_bit_cast(unsigned long long, hi4) & keep_hi);
+      }
+      // Joined as whole vectors: element-wise extraction of these results
+      // miscompiles (it broadcasts element 0) with this toolchain.
+      const op a = __builtin_bit_cast(op, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+      o[mt] = M::mma(a, phi, o[mt]);
+      o[mt] = M::mma(a, plo, o[mt]);
+    }
   }
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
 
-  // 4. Per-wave O tile [16 heads][128] floats into the wave's own area (its V
-  //    reads are done) and per-wave (m, l); then the waves are merged
-  //    (log-sum-exp) for the diagonal blocks (head h, its KV head's 64 dims).
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  float* ot = reinterpret_cast<float*>(warea);
+  // 3. Head r's 64 output dims: tiles 4 kv_r .. 4 kv_r + 3 (its own KV head),
+  //    lane group g holding dims 16 j + 4g .. +3 of tile j.
+  f32x4 od[4];
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ot[(4 * g + i) * kKvd + 16 * nt + r] = o[nt][i];
-  if (g == 0) {
-    red_m(wave)[r] = mw;
-    red_l(wave)[r] = lw;
-  }
-  __syncthreads();
-  if (tid < n_heads) {  // per head: chunk max, merge scale of each wave, sum, 1 / sum
-    const int h = tid;
-    float mx = -INFINITY;
-    for (int w = 0; w < waves; ++w) mx = fmaxf(mx, red_m(w)[h]);
-    float l = 0.0f;
-    for (int w = 0; w < waves; ++w) {
-      const float mwh = red_m(w)[h];
-      const float sc = mwh == -INFINITY ? 0.0f : exp2f(mwh - mx);
-      comb_sc[w * 16 + h] = sc;
-      l = __builtin_fmaf(red_l(w)[h], sc, l);
+  for (int j = 0; j < 4; ++j) od[j] = kv_r ? o[4 + j] : o[j];
+
+  // The chunk's result per (head h, dims 4 d4 .. 4 d4 + 3): a row that fits one
+  // chunk writes `out`; otherwise the chunk's partial (o unnormalised, m in
+  // natural-log units, l) goes to the workspace for decode_merge_kernel.
+  auto emit = [&](const int h, const int d4, const f32x4 acc, const float mh, const float lh) {
+    const size_t head = size_t(t) * n_heads + h;
+    if (single) {
+      *reinterpret_cast<f32x4*>(out + head * 64 + 4 * d4) = acc * (1.0f / lh);
+    } else {
+      const size_t slot = head * num_chunks + c;
+      *reinterpret_cast<f32x4*>(part_o + slot * 64 + 4 * d4) = acc;
+      if (d4 == 0) *reinterpret_cast<float2*>(part_ml + 2 * slot) = make_float2(mh * kLn2, lh);
     }
-    comb_il[h] = 1.0f / l;
-    if (!single) {
-      const size_t slot = (size_t(t) * n_heads + h) * num_chunks + c;
-      part_ml[2 * slot] = mx * kLn2;  // natural-log units
-      part_ml[2 * slot + 1] = l;
-    }
-  }
-  __syncthreads();
-  // Each thread owns outputs idx = tid + k * blockDim (head idx / 64, dim idx % 64).
-#pragma unroll 4
-  for (int idx = tid; idx < n_heads * 64; idx += blockDim.x) {
-    {
-      const int h = idx >> 6, d = idx & 63;
-      const int col = (h >= group ? 64 : 0) + d;
-      float acc = 0.0f;
+  };
+  if constexpr (kOneWave) {
+    if (head_ok) {
 #pragma unroll
-      for (int w = 0; w < kMaxWaves; ++w)
-        if (w < waves)
-          acc = __builtin_fmaf(
-              reinterpret_cast<const float*>(smem + size_t(w) * kWaveLds)[h * kKvd + col],
-              comb_sc[w * 16 + h], acc);
-      const size_t head = size_t(t) * n_heads + h;
-      if (single)
-        out[head * 64 + d] = acc * comb_il[h];
-      else
-        part_o[(head * num_chunks + c) * 64 + d] = acc;
+      for (int j = 0; j < 4; ++j) emit(r, 4 * j + g, od[j], m, l);
+    }
+  } else {
+    // Waves of the workgroup merged by log-sum-exp through LDS: each wave's
+    // output tile [16 heads][64] and its (m, l) per head in its own area (its V
+    // reads are done).
+    const int waves = blockDim.x >> 6;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    float* ot = reinterpret_cast<float*>(warea);
+    float* st = reinterpret_cast<float*>(warea + kOutTile);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(ot + r * 64 + 16 * j + 4 * g) = od[j];
+    if (g == 0) {
+      st[r] = m;
+      st[16 + r] = l;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < n_heads * 16; idx += blockDim.x) {
+      const int h = idx >> 4, d4 = idx & 15;
+      float mx = -INFINITY;
+      for (int w = 0; w < waves; ++w)
+        mx = fmaxf(mx, reinterpret_cast<const float*>(smem + size_t(w) * kTile + kOutTile)[h]);
+      float lsum = 0.0f;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < waves; ++w) {
+        const float* sw = reinterpret_cast<const float*>(smem + size_t(w) * kTile + kOutTile);
+        const float sc = sw[h] == -INFINITY ? 0.0f : exp2f(sw[h] - mx);
+        lsum = __builtin_fmaf(sw[16 + h], sc, lsum);
+        acc += *reinterpret_cast<const f32x4*>(
+                   reinterpret_cast<const float*>(smem + size_t(w) * kTile) + h * 64 + 4 * d4) *
+               sc;
+      }
+      emit(h, d4, acc, mx, lsum);
     }
   }
 }
@@ -327,7 +444,16 @@ bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_d
   return (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) && head_dim == 64 &&
          n_kv_heads * head_dim == kKvd && n_heads <= 16 &&
          n_heads % n_kv_heads == 0 && chunk_tokens % 64 == 0 && chunk_tokens >= 64 &&
-         chunk_tokens <= 512;
+         chunk_tokens <= 1024;
+}
+
+// Waves per workgroup for a chunk: about one wave per 128 positions (a wave
+// streams its positions as page pairs, one pair in flight while it computes the
+// previous one), at most 8, and a whole number of page pairs per wave.
+static int decode_mfma_waves(int chunk_tokens) {
+  int w = std::max(1, std::min(kMaxWaves, chunk_tokens / 128));
+  while (w > 1 && chunk_tokens % (32 * w) != 0) --w;
+  return w;
 }
 
 int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
@@ -335,31 +461,45 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
                 hipStream_t stream) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
-  const int waves = chunk_tokens / 64;
-  const size_t lds = size_t(waves) * kWaveLds;
-  const dim3 grid(T, num_chunks), block(64 * waves);
+  const int waves = decode_mfma_waves(chunk_tokens);
+  const size_t lds = size_t(waves) * kTile;
+  const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
+  if (slots * n_heads * 64 * 4 > 0x7fffffff)
+    return fail(IE_HIP_EINVAL, "attention: split-K workspace above 2 GB (too many rows x chunks)");
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) & 15)
+    return fail(IE_HIP_EINVAL, "attention: q, out and the pools must be 16-byte aligned");
+  const dim3 grid(static_cast<unsigned>(slots)), block(64 * waves);
   const int group = n_heads / n_kv_heads;
   const uint16_t* kp = static_cast<const uint16_t*>(k_pool);
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
-  // 8 waves (512-token chunks) need 128 KB of LDS: above the 64 KB default cap
+  // 8 waves (1024-token chunks) take 128 KB of LDS: above the 64 KB default cap
   // for dynamic LDS, within gfx950's 160 KB per workgroup. Raise it once.
   static const hipError_t attr_f16 = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_F16>),
+      reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_F16, false>),
       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
   static const hipError_t attr_bf16 = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_BF16>),
+      reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_BF16, false>),
       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
   if (int rc = check_hip(kv.kv_dtype == IE_KV_F16 ? attr_f16 : attr_bf16,
                          "hipFuncSetAttribute(attention_partial_mfma)"))
     return rc;
-  if (kv.kv_dtype == IE_KV_F16)
-    hipLaunchKernelGGL(decode_partial_mfma<IE_KV_F16>, grid, block, lds, stream, out, ws.part_o,
-                       ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, kv.max_pages,
-                       kv.num_pages, n_heads, group, num_chunks, chunk_tokens);
-  else
-    hipLaunchKernelGGL(decode_partial_mfma<IE_KV_BF16>, grid, block, lds, stream, out, ws.part_o,
-                       ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, kv.max_pages,
-                       kv.num_pages, n_heads, group, num_chunks, chunk_tokens);
+#define IE_DECODE_LAUNCH(KVT, ONE)                                                              \
+  hipLaunchKernelGGL((decode_partial_mfma<KVT, ONE>), grid, block, lds, stream, out, ws.part_o, \
+                     ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, T, kv.max_pages,      \
+                     kv.num_pages, n_heads, group, num_chunks, chunk_tokens)
+  if (kv.kv_dtype == IE_KV_F16) {
+    if (waves == 1)
+      IE_DECODE_LAUNCH(IE_KV_F16, true);
+    else
+      IE_DECODE_LAUNCH(IE_KV_F16, false);
+  } else {
+    if (waves == 1)
+      IE_DECODE_LAUNCH(IE_KV_BF16, true);
+    else
+      IE_DECODE_LAUNCH(IE_KV_BF16, false);
+  }
+#undef IE_DECODE_LAUNCH
   if (int rc = check_launch("attention_mfma")) return rc;
   return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
 }
