@@ -67,14 +67,27 @@ def fill_pool(torch, n_rows, kv, gen, dev):
 
 
 def time_steps(torch, step, steps, warmup, stream):
+    """Runs `warmup` eager steps, then times exactly `steps` steps, in ms per step.
+
+    The timed steps are recorded once into a HIP graph and replayed: from Python each
+    ctypes launch costs about as much host time as the kernels take on the GPU, so
+    eager launches would measure the host. The library allocates and memsets nothing
+    inside a call, so its launches record as plain kernel nodes. The graph is replayed
+    once untimed, then once between two events on the launch stream.
+    """
     for i in range(warmup):
         step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            step(warmup + i)
+    graph.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for i in range(steps):
-        step(warmup + i)
+    graph.replay()
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps  # ms per step
@@ -83,7 +96,9 @@ def time_steps(torch, step, steps, warmup, stream):
 def cpu_baseline_decode(O, lens, k_host, v_host, tables, kv, q_host, budget_s=10.0):
     """Reference CPU attention per row over a contiguous fp32 gather of its pages."""
     use_ref = O.ref_available()
-    cores = min(O.physical_cores(), 16)
+    # The reference parallelises attention over the query heads only
+    # (src/ops.cpp:78): more than n_heads threads would sit idle.
+    cores = min(O.physical_cores(), NH)
     if use_ref:
         O.ref().ref_set_num_threads(cores)
     gather_s, attn_s, batches = [], [], 0
@@ -140,7 +155,7 @@ def bench_decode(args, torch, ie, O):
     d_tab = torch.from_numpy(tables).to(dev)
     d_pos = torch.from_numpy((lens - 1).astype(np.int32)).to(dev)
     d_seq = torch.arange(B, dtype=torch.int32, device=dev)
-    ct = args.chunk_tokens or 512
+    ct = args.chunk_tokens or ie.attention_chunk_tokens(B, 4096, KV_CODES[kv])
     nc = ie.attention_chunks(4096, ct)
     ws = ie.attention_workspace(B, NH, HD, nc)
     stream = torch.cuda.current_stream()
@@ -156,11 +171,11 @@ def bench_decode(args, torch, ie, O):
     res = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": kv,
         "data": "synthetic",
         "config": {"workload": "config 3: flash-decoding paged attention, batch 64, "
                                "L~U[128,4096], GQA 14q/2kv, head_dim 64, 16-token pages, "
-                               "65,536-page pools, 512-token split-K + LSE merge",
+                               f"65,536-page pools, {ct}-token split-K + LSE merge",
                    "kv_dtype": kv, "batch": B, "chunk_tokens": ct, "num_chunks": nc,
                    "layers_rotated": args.layers, "seed": args.seed,
                    "context_tokens": int(lens.sum())},

@@ -113,9 +113,12 @@ int ie_hip_rope_and_cache(float* q, const float* k, const float* v, void* k_pool
  * Supported: head_dim 64, n_heads/n_kv_heads <= 8 (the reference's limits at
  * this head_dim), page size 16. */
 
-/* Chunk size (tokens, a multiple of 16) that gives T rows of up to
- * `max_context` tokens enough workgroups to fill the device's compute units. */
-int ie_hip_attention_chunk_tokens(int T, int max_context);
+/* Chunk size (tokens, a multiple of 64) for T rows of up to `max_context`
+ * tokens with a KV cache of `kv_dtype`: enough chunks to fill the device's
+ * compute units, sized for the kernel that dtype runs on (matrix-core kernel
+ * for 16-bit caches, VALU kernel for float32). Replaces the reference's fixed
+ * attention_chunks(max_seq_len) sizing (src/cuda/kernels.cu:1387-1391). */
+int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype);
 
 /* Chunks needed to cover `context_tokens` positions: ceil(context/chunk). */
 int ie_hip_attention_chunks(int context_tokens, int chunk_tokens);

@@ -51,7 +51,7 @@ _SIGS = {
     "ie_hip_rope_table": (_i, [_vp, _i, _i, _f]),
     "ie_hip_rope_and_cache": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, KvLayout, _i, _i,
                                    _i, _vp]),
-    "ie_hip_attention_chunk_tokens": (_i, [_i, _i]),
+    "ie_hip_attention_chunk_tokens": (_i, [_i, _i, _i]),
     "ie_hip_attention_chunks": (_i, [_i, _i]),
     "ie_hip_attention_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i]),
     "ie_hip_attention": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _vp, _i, _i, _i,
@@ -161,8 +161,9 @@ def rope_and_cache(q, k, v, k_pool, v_pool, table, row_pos, row_seq, tables, max
                                        _stream(stream)))
 
 
-def attention_chunk_tokens(T: int, max_context: int) -> int:
-    return int(lib().ie_hip_attention_chunk_tokens(T, max_context))
+def attention_chunk_tokens(T: int, max_context: int, kv_dtype: int = KV_F16) -> int:
+    """Chunk size for T rows of up to max_context tokens (kv_dtype picks the kernel)."""
+    return int(lib().ie_hip_attention_chunk_tokens(T, max_context, kv_dtype))
 
 
 def attention_chunks(context: int, chunk_tokens: int) -> int:

@@ -210,17 +210,26 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
   }
 }
 
-// One workgroup per (head, row), one thread per output dim. The partials of up
-// to 32 chunks are loaded together (independent loads, one memory round trip),
-// then combined: M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L.
-// Longer rows take further batches with the running (M, L, acc) rescaled.
+// One workgroup per (head, row), one lane per output dim, and as many waves as
+// it takes to give each wave at most 32 of the row's chunks (up to 16 waves):
+// wave w takes chunks w, w + W, w + 2W, ... Each lane first reads the row's
+// position (its chunk count), then loads its wave's partials -- up to 32
+// chunks, all in flight at once -- and combines them:
+//   M = max m_c, L = sum l_c e^(m_c - M), acc = sum o_c e^(m_c - M);
+// longer rows take further batches with the running (M, L, acc) rescaled. The
+// waves' (M, L, acc) are combined the same way through LDS: out = acc / L.
+constexpr int kMergeBatch = 32;
+constexpr int kMergeMaxWaves = 16;
+
 template <int HD>
-__global__ void __launch_bounds__(HD)
+__global__ void __launch_bounds__(HD * kMergeMaxWaves)
 decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
                     const float* __restrict__ part_ml, const int32_t* __restrict__ row_pos,
                     int n_heads, int num_chunks, int chunk_tokens) {
-  constexpr int kBatch = 32;
-  const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  __shared__ float red_m[kMergeMaxWaves], red_l[kMergeMaxWaves];
+  __shared__ float red_a[kMergeMaxWaves][HD];
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int d = threadIdx.x % HD, w = threadIdx.x / HD, W = blockDim.x / HD;
   const int p = row_pos[t];
   if (p < 0) return;
   const int nc = min(p / chunk_tokens + 1, num_chunks);
@@ -228,30 +237,52 @@ decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
   const size_t base = (size_t(t) * n_heads + h) * num_chunks;
   const float2* ml = reinterpret_cast<const float2*>(part_ml) + base;
   float M = -INFINITY, L = 0.0f, acc = 0.0f;
-  for (int c0 = 0; c0 < nc; c0 += kBatch) {
-    float2 mlc[kBatch];
-    float oc[kBatch];
+  for (int c0 = w; c0 < nc; c0 += kMergeBatch * W) {
+    float2 mlc[kMergeBatch];
+    float oc[kMergeBatch];
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const bool ok = c0 + j < nc;
-      mlc[j] = ok ? ml[c0 + j] : make_float2(-INFINITY, 0.0f);
-      oc[j] = ok ? part_o[(base + c0 + j) * HD + d] : 0.0f;
+    for (int j = 0; j < kMergeBatch; ++j) {
+      const int c = c0 + j * W;
+      const bool ok = c < nc;
+      mlc[j] = ok ? ml[c] : make_float2(-INFINITY, 0.0f);
+      oc[j] = ok ? part_o[(base + c) * HD + d] : 0.0f;
     }
     float mb = M;
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, mlc[j].x);
+    for (int j = 0; j < kMergeBatch; ++j) mb = fmaxf(mb, mlc[j].x);
+    if (mb == -INFINITY) continue;  // no visible position yet
     const float sc = M == -INFINITY ? 0.0f : expf(M - mb);
     L *= sc;
     acc *= sc;
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const float w = c0 + j < nc ? expf(mlc[j].x - mb) : 0.0f;
-      L = __builtin_fmaf(mlc[j].y, w, L);
-      acc = __builtin_fmaf(oc[j], w, acc);
+    for (int j = 0; j < kMergeBatch; ++j) {
+      const float e = c0 + j * W < nc ? expf(mlc[j].x - mb) : 0.0f;
+      L = __builtin_fmaf(mlc[j].y, e, L);
+      acc = __builtin_fmaf(oc[j], e, acc);
     }
     M = mb;
   }
-  out[(size_t(t) * n_heads + h) * HD + d] = acc / L;
+  const size_t o = (size_t(t) * n_heads + h) * HD + d;
+  if (W == 1) {
+    out[o] = acc / L;
+    return;
+  }
+  if (d == 0) {
+    red_m[w] = M;
+    red_l[w] = L;
+  }
+  red_a[w][d] = acc;
+  __syncthreads();
+  if (w != 0) return;
+  float mx = -INFINITY;
+  for (int i = 0; i < W; ++i) mx = fmaxf(mx, red_m[i]);
+  float lt = 0.0f, at = 0.0f;
+  for (int i = 0; i < W; ++i) {
+    const float e = red_m[i] == -INFINITY ? 0.0f : expf(red_m[i] - mx);
+    lt = __builtin_fmaf(red_l[i], e, lt);
+    at = __builtin_fmaf(red_a[i][d], e, at);
+  }
+  out[o] = at / lt;
 }
 
 template <int KV, int G>
@@ -300,7 +331,9 @@ int dispatch_group(int group, float* out, const float* q, const void* k_pool, co
 int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T, int n_heads,
                  int num_chunks, int chunk_tokens, hipStream_t stream) {
   if (num_chunks <= 1) return IE_HIP_OK;
-  hipLaunchKernelGGL((decode_merge_kernel<64>), dim3(n_heads, T), dim3(64), 0, stream, out,
+  const int waves =
+      std::min(kMergeMaxWaves, std::max(1, (num_chunks + kMergeBatch - 1) / kMergeBatch));
+  hipLaunchKernelGGL((decode_merge_kernel<64>), dim3(n_heads, T), dim3(64 * waves), 0, stream, out,
                      ws.part_o, ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
   return check_launch("attention_merge");
 }
@@ -368,11 +401,20 @@ int ie_hip_attention_chunks(int context_tokens, int chunk_tokens) {
   return (context_tokens + chunk_tokens - 1) / chunk_tokens;
 }
 
-int ie_hip_attention_chunk_tokens(int T, int max_context) {
+int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
   const int cus = device_compute_units();
+  const int64_t rows = std::max(T, 1);
+  const int ctx = std::max(max_context, 1);
+  if (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) {
+    // Matrix-core kernel: one-wave workgroups streaming 128 positions each fill
+    // the device best (measured on MI355X); 64 when that leaves fewer than two
+    // workgroups per compute unit.
+    return rows * ie_hip_attention_chunks(ctx, 128) >= 2 * cus ? 128 : 64;
+  }
+  // float32 VALU kernel: the largest chunk that still gives every compute unit
+  // a workgroup.
   for (int ct : {512, 256, 128, 64})
-    if (int64_t(std::max(T, 1)) * ie_hip_attention_chunks(std::max(max_context, 1), ct) >= cus)
-      return ct;
+    if (rows * ie_hip_attention_chunks(ctx, ct) >= cus) return ct;
   return 64;
 }
 

@@ -191,3 +191,49 @@ def test_mfma_forced_and_shape_limits(ie, O, dev, kv):
             gpu_attention(ie, dev, q, kp, vp, kvt, pos, seq, tables, max_pages, 48)
     finally:
         ie.set_attention_impl(prev)
+
+
+@pytest.mark.parametrize("kv", ["f16", "f32"])
+def test_graph_replay_matches_eager(ie, O, dev, kv):
+    """A decode step (append + attention) recorded into a HIP graph replays to the eager
+    result every time, with eager work and synchronisations between the replays (the
+    library records no memset nodes: every node is one of its kernels)."""
+    kvt = KVS[kv]
+    rng = np.random.default_rng(31)
+    lens = [700, 1300, 90, 2049]
+    tables, max_pages, num_pages = make_tables(lens, rng, extra_pages=2)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_pos = np.array([n - 1 for n in lens], np.int32)
+    row_seq = np.arange(len(lens), dtype=np.int32)
+    q, k, v = normal(rng, (4, QD)), normal(rng, (4, KVD)), normal(rng, (4, KVD))
+    table = ie.rope_table(4096, HD, 1e6).to(dev)
+    dkp, dvp = to_dev(kp, dev, kvt), to_dev(vp, dev, kvt)
+    dtab, dpos, dseq = to_dev(tables, dev), to_dev(row_pos, dev), to_dev(row_seq, dev)
+    dk, dv = to_dev(k, dev), to_dev(v, dev)
+    ct = ie.attention_chunk_tokens(4, 4096, kvt)
+    nc = ie.attention_chunks(4096, ct)
+    ws = ie.attention_workspace(4, NH, HD, nc)
+    q0 = to_dev(q, dev)
+    dq = q0.clone()
+    out = torch.empty((4, QD), dtype=torch.float32, device=dev)
+
+    def step():
+        dq.copy_(q0)
+        ie.rope_and_cache(dq, dk, dv, dkp, dvp, table, dpos, dseq, dtab, max_pages, NH, NKV, HD)
+        ie.attention(out, dq, dkp, dvp, dpos, dseq, dtab, max_pages, nc, ct, ws, NH, NKV, HD)
+
+    step()
+    torch.cuda.synchronize()
+    eager = from_dev(out).copy()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for i in range(4):
+        out.fill_(float("nan"))
+        scratch = torch.randn(1 << 20, device=dev).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = from_dev(out)
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {i}"
+    del scratch
