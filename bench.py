@@ -66,6 +66,9 @@ def fill_pool(torch, n_rows, kv, gen, dev):
     return torch.randn((n_rows, KVD), generator=gen, device=dev, dtype=dt)
 
 
+EAGER = False  # --eager: launch every timed step from Python (for counter collection)
+
+
 def time_steps(torch, step, steps, warmup, stream):
     """Runs `warmup` eager steps, then times exactly `steps` steps, in ms per step.
 
@@ -78,6 +81,15 @@ def time_steps(torch, step, steps, warmup, stream):
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
+    if EAGER:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            step(warmup + i)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(steps):
@@ -289,10 +301,15 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true", help="config 2: rows-per-launch sweep")
     ap.add_argument("--probe", action="store_true", help="also measure device copy bandwidth")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the timed steps one by one instead of replaying a graph "
+                         "(host-bound timing; for rocprofv3 counter runs)")
     ap.add_argument("--probe-only", action="store_true",
                     help="only the device copy (the plain copy kernel that rocprofv3 byte "
                          "counters are calibrated on)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this path has no multi-GPU mode (the paged KV "
               "cache would shard by sequence, one pool per GPU, with no exchange); run with "
