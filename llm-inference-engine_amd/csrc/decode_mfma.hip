@@ -59,14 +59,10 @@
 
 #include "common.hpp"
 #include "decode.hpp"
+#include "mfma.hpp"
 
 namespace iehip {
 namespace {
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short s4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKvd = 128;          // elements per KV row (n_kv_heads * 64)
 constexpr int kPair = 8192;        // one V page-pair tile [32 tok][256 B]
@@ -77,35 +73,6 @@ constexpr int kOutTile = 16 * 64 * 4;        // a wave's output tile [16 heads][
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxLds = kMaxWaves * kTile;
-
-template <int KV>
-struct Mfma;
-
-template <>
-struct Mfma<IE_KV_F16> {
-  using op = f16x8;
-  using elem = _Float16;
-  __device__ __forceinline__ static f32x4 mma(op a, op b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <>
-struct Mfma<IE_KV_BF16> {
-  using op = bf16x8;
-  using elem = __bf16;
-  __device__ __forceinline__ static f32x4 mma(op a, op b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-
-// s_waitcnt with only the vector-memory counter set (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14, expcnt and lgkmcnt left at their "no wait" maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 #pragma unroll
@@ -250,10 +217,10 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     for (int k = 0; k < 2; ++k)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float v = x[k][j] * qs;
-        const E hi = static_cast<E>(v);
+        E hi, lo;
+        split16(x[k][j] * qs, hi, lo);
         h2[k][j] = hi;
-        l2[k][j] = static_cast<E>(v - static_cast<float>(hi));
+        l2[k][j] = lo;
       }
     const op zero = {};
 #pragma unroll
@@ -319,11 +286,13 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     for (int i = 0; i < 4; ++i) {
       const float ea = exp2f(sa[i] - mref), eb = exp2f(sb[i] - mref);
       sum += ea + eb;
-      const E ha = static_cast<E>(ea), hb = static_cast<E>(eb);
+      E ha, la, hb, lb;
+      split16(ea, ha, la);
+      split16(eb, hb, lb);
       phi[i] = ha;
       phi[4 + i] = hb;
-      plo[i] = static_cast<E>(ea - static_cast<float>(ha));
-      plo[4 + i] = static_cast<E>(eb - static_cast<float>(hb));
+      plo[i] = la;
+      plo[4 + i] = lb;
     }
     if (j == 0) {
       l = sum;
@@ -359,17 +328,13 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       const int slot = 2 * (mt ^ rsw) + rpc;
-      s4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s4*)(vt + slot * 16));
-      s4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s4*)(vt + 16 * 256 + slot * 16));
+      s16x4 lo4 = lds_read_tr16(vt + slot * 16);
+      s16x4 hi4 = lds_read_tr16(vt + 16 * 256 + slot * 16);
       if (!full) {
-        lo4 = __builtin_bit_cast(s4, __builtin_bit_cast(unsigned long long, lo4) & keep_lo);
-        hi4 = __builtin_bit_cast(s4, __builtin_bit_cast(unsigned long long, hi4) & keep_hi);
+        lo4 = __builtin_bit_cast(s16x4, __builtin_bit_cast(unsigned long long, lo4) & keep_lo);
+        hi4 = __builtin_bit_cast(s16x4, __builtin_bit_cast(unsigned long long, hi4) & keep_hi);
       }
-      // Joined as whole vectors: element-wise extraction of these results
-      // miscompiles (it broadcasts element 0) with this toolchain.
-      const op a = __builtin_bit_cast(op, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+      const op a = join_tr<op>(lo4, hi4);
       o[mt] = M::mma(a, phi, o[mt]);
       o[mt] = M::mma(a, plo, o[mt]);
     }

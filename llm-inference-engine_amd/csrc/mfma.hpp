@@ -1,0 +1,70 @@
+// Matrix-core (MFMA) building blocks shared by the gfx950 attention kernels:
+// 16-bit operand types, the 16x16x32 products in the KV cache's own 16-bit
+// type, and an s_waitcnt on the vector-memory counter alone.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "ie_hip.h"
+
+namespace iehip {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// D = A[16x32] . B[32x16] + C, float32 accumulation. Operand lane layout:
+// lane (g, r) = (lane / 16, lane % 16) holds A[r][8g .. 8g+7] and B[8g .. 8g+7][r];
+// the result lane (g, r) holds D[4g .. 4g+3][r].
+template <int KV>
+struct Mfma;
+
+template <>
+struct Mfma<IE_KV_F16> {
+  using op = f16x8;
+  using elem = _Float16;
+  __device__ __forceinline__ static f32x4 mma(op a, op b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<IE_KV_BF16> {
+  using op = bf16x8;
+  using elem = __bf16;
+  __device__ __forceinline__ static f32x4 mma(op a, op b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// s_waitcnt with only the vector-memory counter set (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt and lgkmcnt left at their "no wait" maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane 4a+b
+// receives element b of the 8-byte reads of lanes a, a+4, a+8, a+12.
+__device__ __forceinline__ s16x4 lds_read_tr16(const unsigned char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
+// Two transposing reads joined into one 8-element operand. Joined as whole
+// vectors: element-wise extraction of these results miscompiles (it
+// broadcasts element 0) with this toolchain.
+template <typename Op>
+__device__ __forceinline__ Op join_tr(s16x4 lo, s16x4 hi) {
+  return __builtin_bit_cast(Op, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// x = hi + lo in the 16-bit type E, |x - hi - lo| ~ 2^-22 |x|.
+template <typename E>
+__device__ __forceinline__ void split16(float x, E& hi, E& lo) {
+  hi = static_cast<E>(x);
+  lo = static_cast<E>(x - static_cast<float>(hi));
+}
+
+}  // namespace iehip

@@ -190,9 +190,13 @@ int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, con
   if (T == 0) return IE_HIP_OK;
   if (!out || !q || !k_pool || !v_pool || !row_pos || !row_seq)
     return fail(IE_HIP_EINVAL, "attention_prefill: null pointer");
-  if (kv.kv_dtype != IE_KV_F32 && attention_impl() != IE_HIP_IMPL_VALU && prefill_mfma_enabled())
+  const int impl = attention_impl();
+  if (impl != IE_HIP_IMPL_VALU && prefill_mfma_enabled() &&
+      prefill_mfma_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim))
     return prefill_mfma_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads,
                                n_kv_heads, stream);
+  if (impl == IE_HIP_IMPL_MFMA)
+    return fail(IE_HIP_EINVAL, "attention_prefill: the MFMA kernel needs a 16-bit KV cache");
   return prefill_valu_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads, n_kv_heads,
                              stream);
 }

@@ -237,3 +237,30 @@ def test_graph_replay_matches_eager(ie, O, dev, kv):
         got = from_dev(out)
         assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {i}"
     del scratch
+
+
+@pytest.mark.parametrize("kv", list(KVS))
+def test_stale_nonfinite_pool_rows_do_not_leak(ie, O, dev, kv, impl):
+    """Pool rows the attention must not see -- the tail of each row's last page, every
+    other page of the pool -- hold inf and NaN; outputs stay finite and match the oracle
+    (which only ever reads positions 0..p)."""
+    kvt = KVS[kv]
+    rng = np.random.default_rng(43)
+    lens = [37, 200, 1, 130]
+    tables, max_pages, num_pages = make_tables(lens, rng, extra_pages=3)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    used = np.zeros(num_pages * 16, bool)
+    for s_, n in enumerate(lens):
+        for p_ in range(n):
+            used[tables[s_, p_ // 16] * 16 + p_ % 16] = True
+    poison = O.round_to_kv(np.resize(np.array([np.nan, np.inf], np.float32),
+                                     (int((~used).sum()), KVD)).astype(np.float32), kvt)
+    kp[~used] = poison
+    vp[~used] = poison
+    row_pos = np.array([n - 1 for n in lens], np.int32)
+    row_seq = np.arange(len(lens), dtype=np.int32)
+    q = normal(rng, (len(lens), QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD)
+    for ct in (64, 128, 256):
+        got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct)
+        check(O, got, want, kvt, f"chunk {ct}")

@@ -20,6 +20,14 @@ pytestmark = pytest.mark.gpu
 KVS = {"f32": 0, "f16": 1, "bf16": 2}
 
 
+@pytest.fixture(params=["auto", "valu"])
+def impl(request, ie):
+    """Runs a test with the default kernels (MFMA for 16-bit caches) and with the VALU ones."""
+    prev = ie.set_attention_impl({"auto": ie.IMPL_AUTO, "valu": ie.IMPL_VALU}[request.param])
+    yield request.param
+    ie.set_attention_impl(prev)
+
+
 def gpu_prefill(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages):
     out = torch.full((len(row_pos), QD), float("nan"), dtype=torch.float32, device=dev)
     ie.attention_prefill(out, to_dev(q, dev), to_dev(kp, dev, kvt), to_dev(vp, dev, kvt),
@@ -42,7 +50,7 @@ PROMPTS = [
 
 @pytest.mark.parametrize("case", range(len(PROMPTS)))
 @pytest.mark.parametrize("kv", list(KVS))
-def test_prompts(ie, O, dev, case, kv):
+def test_prompts(ie, O, dev, case, kv, impl):
     lens, seq, start, T = PROMPTS[case]
     kvt = KVS[kv]
     rng = np.random.default_rng(200 + case)
@@ -60,7 +68,7 @@ def test_prompts(ie, O, dev, case, kv):
 
 
 @pytest.mark.parametrize("kv", ["f16", "bf16"])
-def test_config5_prefill_4000_into_churned_pool(ie, O, dev, kv):
+def test_config5_prefill_4000_into_churned_pool(ie, O, dev, kv, impl):
     """BASELINE config 5 (prefill half): 25% of a pool's pages freed and re-allocated from a
     seeded free list, then a 4,000-token chunk appended into fresh pages (RoPE+append kernel)
     and attended causally. Pages are checked bit-exactly; attention on sampled rows."""
@@ -102,3 +110,49 @@ def test_config5_prefill_4000_into_churned_pool(ie, O, dev, kv):
     want = O.paged_attention(q_rot[sample], kp_ref, vp_ref, kvt, row_pos[sample], row_seq[sample],
                              tables, max_pages, NH, NKV, HD, threads=8)
     check(O, from_dev(out)[sample], want, kvt, "config 5 prefill")
+
+
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_mfma_forced_and_shape_limits(ie, O, dev, kv):
+    """IMPL_MFMA runs the matrix-core prefill kernel; an f32 cache then fails loudly."""
+    kvt = KVS[kv]
+    rng = np.random.default_rng(41)
+    tables, max_pages, num_pages = make_tables([333], rng)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_pos = np.arange(100, 333, dtype=np.int32)
+    row_seq = np.zeros(len(row_pos), np.int32)
+    q = normal(rng, (len(row_pos), QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
+                             threads=8)
+    prev = ie.set_attention_impl(ie.IMPL_MFMA)
+    try:
+        check(O, gpu_prefill(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages), want,
+              kvt)
+        kf = O.widen_kv(kp, kvt)
+        with pytest.raises(ie.IeHipError):
+            gpu_prefill(ie, dev, q, kf, kf, 0, row_pos, row_seq, tables, max_pages)
+    finally:
+        ie.set_attention_impl(prev)
+
+
+@pytest.mark.parametrize("kv", list(KVS))
+def test_stale_nonfinite_pool_rows_do_not_leak(ie, O, dev, kv, impl):
+    """Prefill over a pool whose rows past the prompt (and all unused pages) hold inf/NaN."""
+    kvt = KVS[kv]
+    rng = np.random.default_rng(44)
+    L = 150  # the sequence's pages cover 160 positions; 150..159 are stale
+    tables, max_pages, num_pages = make_tables([L + 10], rng, extra_pages=2)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    used = np.zeros(num_pages * 16, bool)
+    for p_ in range(L):
+        used[tables[0, p_ // 16] * 16 + p_ % 16] = True
+    poison = O.round_to_kv(np.resize(np.array([np.inf, np.nan], np.float32),
+                                     (int((~used).sum()), KVD)).astype(np.float32), kvt)
+    kp[~used] = poison
+    vp[~used] = poison
+    row_pos = np.arange(40, L, dtype=np.int32)
+    row_seq = np.zeros(len(row_pos), np.int32)
+    q = normal(rng, (len(row_pos), QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD)
+    check(O, gpu_prefill(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages), want, kvt,
+          "stale rows")
