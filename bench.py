@@ -16,7 +16,10 @@ reference's own CPU attention (oracle/_ref: src/ops.cpp + src/threadpool.cpp,
 -O3 -mavx2 -mfma) on the same batch, rows gathered to contiguous fp32 first
 (gather timed separately), on this host's cores.
 
-Other configs (--config 2|4|5) print the same JSON shape for DESIGN.md tables.
+Other configs print the same JSON shape for the tables in DESIGN.md:
+  --config 2  RoPE + paged append, 64 rows (+ --sweep: rows per launch up to 131,072)
+  --config 4  long-context decode, 24 layers, batch 1, 32k context, bf16
+  --config 5  mixed step: 48 decode rows + a 4,000-token prefill (MFMA), f16
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 """
 from __future__ import annotations
@@ -257,6 +260,148 @@ def bench_append(args, torch, ie, O):
     }
 
 
+def bench_long(args, torch, ie, O):
+    """Config 4: long-context decode, all 24 layers. Batch 1, context 32,768, bf16 KV in
+    shuffled 16-token pages (one pool per layer), per layer a RoPE + append at position
+    32,767 then attention over the 32,768 positions."""
+    dev = torch.device("cuda:0")
+    kv = args.kv or "bf16"
+    rng = np.random.default_rng(args.seed)
+    layers, L = 24, 32768
+    pages = L // PAGE
+    num_pages = 2 * pages  # half of each pool unused, so the row's pages are scattered
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    k_pools = [fill_pool(torch, num_pages * PAGE, kv, gen, dev) for _ in range(layers)]
+    v_pools = [fill_pool(torch, num_pages * PAGE, kv, gen, dev) for _ in range(layers)]
+    tabs = [torch.from_numpy(rng.permutation(num_pages)[:pages].astype(np.int32)[None, :]).to(dev)
+            for _ in range(layers)]
+    table = ie.rope_table(L, HD, THETA).to(dev)
+    q = torch.randn((layers, 1, QD), generator=gen, device=dev)
+    k = torch.randn((layers, 1, KVD), generator=gen, device=dev)
+    v = torch.randn((layers, 1, KVD), generator=gen, device=dev)
+    out = torch.empty((1, QD), device=dev)
+    d_pos = torch.tensor([L - 1], dtype=torch.int32, device=dev)
+    d_seq = torch.zeros(1, dtype=torch.int32, device=dev)
+    ct = args.chunk_tokens or ie.attention_chunk_tokens(1, L, KV_CODES[kv])
+    nc = ie.attention_chunks(L, ct)
+    ws = ie.attention_workspace(1, NH, HD, nc)
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        for l in range(layers):
+            ie.rope_and_cache(q[l], k[l], v[l], k_pools[l], v_pools[l], table, d_pos, d_seq,
+                              tabs[l], pages, NH, NKV, HD)
+            ie.attention(out, q[l], k_pools[l], v_pools[l], d_pos, d_seq, tabs[l], pages, nc, ct,
+                         ws, NH, NKV, HD)
+
+    ms = time_steps(torch, step, args.steps, args.warmup, stream)
+    per_layer = 2 * KVD * KV_BYTES[kv] * L + 2 * QD * 4 + 4 * pages + 8 + \
+        (1024 + 2 * KVD * KV_BYTES[kv] + 12 + 2 * QD * 4)
+    nbytes = layers * per_layer
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "long-context decode step (24 layers, batch 1, 32k context) GB/s, 1 GPU",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": kv, "data": "synthetic",
+        "config": {"workload": "config 4: 24 layers x (RoPE+append at 32,767, flash-decoding "
+                               "over 32,768 positions), batch 1, shuffled 16-token pages",
+                   "kv_dtype": kv, "chunk_tokens": ct, "num_chunks": nc, "seed": args.seed},
+        "tok_per_s": round(1 / (ms * 1e-3), 1), "us_per_layer": round(ms * 1e3 / layers, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "algorithmic_bytes_per_step": nbytes,
+    }
+
+
+def bench_mixed(args, torch, ie, O):
+    """Config 5: one mixed serving step of one layer -- 48 decode rows (contexts
+    U[256, 2048]) plus a 4,000-token chunked prefill written into fresh pages of a pool
+    whose pages were churned (25% freed and re-allocated) first; f16 KV."""
+    dev = torch.device("cuda:0")
+    kv = args.kv or "f16"
+    rng = np.random.default_rng(args.seed)
+    num_pages, max_seq, n_dec, P = 65536, 8192, 48, 4000
+    pool = ie.PagePool(num_pages, 64, max_seq)
+    seqs = [pool.open_sequence() for _ in range(64)]
+    lens = {s: int(rng.integers(256, 2049)) for s in seqs}
+    for s in seqs:
+        pool.ensure(s, lens[s])
+    for s in rng.permutation(seqs)[:16]:  # 25% of the sequences finish: their pages go back
+        pool.close_sequence(int(s))
+        del lens[int(s)]
+    dec = sorted(lens)[:n_dec]
+    pf = pool.open_sequence()
+    pool.ensure(pf, P)  # fresh pages for the prompt, most of them the freed ones
+    for s in dec:       # each decode row appends its next token
+        pool.ensure(s, lens[s] + 1)
+    max_pages = pool.max_pages_per_seq
+    d_tab = torch.zeros(pool.max_batch * max_pages, dtype=torch.int32, device=dev)
+    pool.upload_tables(d_tab)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    k_pool = fill_pool(torch, num_pages * PAGE, kv, gen, dev)
+    v_pool = fill_pool(torch, num_pages * PAGE, kv, gen, dev)
+    table = ie.rope_table(max_seq, HD, THETA).to(dev)
+    pq, pk, pv = (torch.randn((P, d), generator=gen, device=dev) for d in (QD, KVD, KVD))
+    dq, dk, dv = (torch.randn((n_dec, d), generator=gen, device=dev) for d in (QD, KVD, KVD))
+    p_pos = torch.arange(P, dtype=torch.int32, device=dev)
+    p_seq = torch.full((P,), pf, dtype=torch.int32, device=dev)
+    d_pos = torch.tensor([lens[s] for s in dec], dtype=torch.int32, device=dev)
+    d_seq = torch.tensor(dec, dtype=torch.int32, device=dev)
+    p_out = torch.empty((P, QD), device=dev)
+    d_out = torch.empty((n_dec, QD), device=dev)
+    ct = args.chunk_tokens or ie.attention_chunk_tokens(n_dec, 2049, KV_CODES[kv])
+    nc = ie.attention_chunks(2049, ct)
+    ws = ie.attention_workspace(n_dec, NH, HD, nc)
+    stream = torch.cuda.current_stream()
+
+    def prefill(i):
+        ie.rope_and_cache(pq, pk, pv, k_pool, v_pool, table, p_pos, p_seq, d_tab, max_pages,
+                          NH, NKV, HD)
+        ie.attention_prefill(p_out, pq, k_pool, v_pool, p_pos, p_seq, d_tab, max_pages, NH, NKV,
+                             HD)
+
+    def prefill_attn(i):
+        ie.attention_prefill(p_out, pq, k_pool, v_pool, p_pos, p_seq, d_tab, max_pages, NH, NKV,
+                             HD)
+
+    def decode(i):
+        ie.rope_and_cache(dq, dk, dv, k_pool, v_pool, table, d_pos, d_seq, d_tab, max_pages,
+                          NH, NKV, HD)
+        ie.attention(d_out, dq, k_pool, v_pool, d_pos, d_seq, d_tab, max_pages, nc, ct, ws, NH,
+                     NKV, HD)
+
+    def step(i):
+        prefill(i)
+        decode(i)
+
+    ms = time_steps(torch, step, args.steps, args.warmup, stream)
+    ms_pf = time_steps(torch, prefill_attn, args.steps, args.warmup, stream)
+    ms_dec = time_steps(torch, decode, args.steps, args.warmup, stream)
+    flops = 4 * NH * HD * P * (P + 1) // 2
+    tflops = flops / (ms_pf * 1e-3) / 1e12
+    dec_bytes = decode_bytes([lens[s] + 1 for s in dec], KV_BYTES[kv])
+    return {
+        "metric": "mixed serving step (48 decode rows + 4,000-token prefill, one layer), 1 GPU",
+        "value": round((n_dec + P) / (ms * 1e-3), 1), "unit": "rows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": kv,
+        "data": "synthetic",
+        "config": {"workload": "config 5: 48 decode rows (L~U[256,2048]) + one 4,000-token "
+                               "prefill into fresh pages after 25% page churn, one layer",
+                   "kv_dtype": kv, "chunk_tokens": ct, "seed": args.seed},
+        "prefill_attention_ms": round(ms_pf, 5),
+        "prefill_tflops": round(tflops, 2),
+        "decode_part_ms": round(ms_dec, 5),
+        "decode_part_gbs": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "kernel": "attention_prefill (causal 4,000 x 4,000, 28.7 GFLOP)"},
+    }
+
+
 def traffic_from_profiles(kernel: str):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE runs, as committed
     under profiles/ (null when that measurement has not been made)."""
@@ -291,7 +436,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=3, choices=[2, 3])
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
     ap.add_argument("--kv", choices=list(KV_CODES), default=None)
     ap.add_argument("--chunk-tokens", type=int, default=None)
     ap.add_argument("--layers", type=int, default=8)
@@ -329,7 +474,8 @@ def main():
         print(json.dumps({"measured_copy_gbs": copy_probe(torch), "copy_bytes": 2 << 30}),
               flush=True)
         return
-    res = bench_decode(args, torch, ie, O) if args.config == 3 else bench_append(args, torch, ie, O)
+    res = {2: bench_append, 3: bench_decode, 4: bench_long, 5: bench_mixed}[args.config](
+        args, torch, ie, O)
     if args.probe:
         res["measured_copy_gbs"] = copy_probe(torch)
     print(json.dumps(res), flush=True)

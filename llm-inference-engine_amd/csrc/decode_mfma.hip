@@ -284,7 +284,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float ea = exp2f(sa[i] - mref), eb = exp2f(sb[i] - mref);
+      const float ea = exp2_weight(sa[i] - mref), eb = exp2_weight(sb[i] - mref);
       sum += ea + eb;
       E ha, la, hb, lb;
       split16(ea, ha, la);
@@ -297,7 +297,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     if (j == 0) {
       l = sum;
     } else {
-      const float corr = exp2f(m - mref);  // m = -inf (nothing seen yet): 0
+      const float corr = exp2_weight(m - mref);  // m = -inf (nothing seen yet): 0
       l = __builtin_fmaf(l, corr, sum);
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) o[mt] *= corr;

@@ -60,11 +60,17 @@ __device__ __forceinline__ Op join_tr(s16x4 lo, s16x4 hi) {
   return __builtin_bit_cast(Op, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// x = hi + lo in the 16-bit type E, |x - hi - lo| ~ 2^-22 |x|.
+// x = hi + lo in the 16-bit type E, |x - hi - lo| ~ 2^-22 |x|. x - hi is exact in
+// float32; written as an fma of the widened hi so that for f16 it becomes one
+// mixed-precision v_fma_mix (f32 and f16 sources, f16 result).
 template <typename E>
 __device__ __forceinline__ void split16(float x, E& hi, E& lo) {
   hi = static_cast<E>(x);
-  lo = static_cast<E>(x - static_cast<float>(hi));
+  lo = static_cast<E>(__builtin_fmaf(-1.0f, static_cast<float>(hi), x));
 }
+
+// 2^x for the softmax weights: the bare v_exp_f32 (x <= 0 here; results below
+// 2^-126, where it may flush to zero, are far below the weights' tolerance).
+__device__ __forceinline__ float exp2_weight(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace iehip

@@ -23,14 +23,15 @@
 // Layout of the work:
 //   One workgroup per (pair of 16-row blocks, KV head); one wave per query head
 //   of the KV head (the 7 heads of a Qwen2.5 group share every K/V tile through
-//   LDS). The pair is block b and block n-1-b: the causal triangle gives block b
+//   LDS). Two heads per wave (each K/V operand feeding both) was measured
+//   slower: half the waves leave the dependency and barrier stalls exposed. The pair is block b and block n-1-b: the causal triangle gives block b
 //   b+1 key tiles of work, so every pair carries about the same total and the
 //   ceil(n/2) x n_kv_heads workgroups finish together (the heavier block goes
 //   first).
-//   K/V tiles of 64 keys (4 pages) are double-buffered in LDS (2 x 16 KB): while
-//   the waves compute on one, the next tile's 16 KB arrive by DMA
-//   (global_load_lds_dwordx4, 16 x 1 KB spread over the waves), page ids
-//   prefetched a tile ahead. K rows are stored with their 16-byte pieces
+//   K/V tiles of 64 keys (4 pages) go through a ring of 4 LDS buffers (4 x 16 KB):
+//   while the waves compute on one, the next three tiles' 16 KB each are in
+//   flight by DMA (global_load_lds_dwordx4, 16 x 1 KB spread evenly over the waves),
+//   page ids read a tile ahead. K rows are stored with their 16-byte pieces
 //   swizzled (piece ^ (row/2 % 8)) so the A-operand reads (16 rows, one piece
 //   each) hit distinct banks; V rows with piece ^ 2*(row/2 % 4) so the
 //   transposed reads (ds_read_b64_tr_b16: 8 rows x 32 bytes per half-wave) do.
@@ -50,12 +51,16 @@ constexpr int kRows = 16;                  // query rows per block (one MFMA col
 constexpr int kKeys = 64;                  // keys per LDS tile
 constexpr int kTileBytes = kKeys * 128;    // 64 keys x 64 dims x 2 B
 constexpr int kBufBytes = 2 * kTileBytes;  // K tile + V tile
-constexpr int kLdsBytes = 2 * kBufBytes;   // double-buffered
+constexpr int kRing = 4;                   // tiles in LDS: one computed, three in flight
+constexpr int kLdsBytes = kRing * kBufBytes;
 constexpr int kMaxGroup = 8;
+constexpr int kHeadsPerWave = 1;           // query heads per wave (2 measured slower: fewer waves)
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int KV>
-__global__ void __launch_bounds__(64 * kMaxGroup)
+// kWaves = group / kHeadsPerWave waves (rounded up), wave w taking query heads
+// kHeadsPerWave * w .. of the KV head.
+template <int KV, int kWaves>
+__global__ void __launch_bounds__(64 * kWaves)
 prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
                     const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
                     int T, const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
@@ -64,12 +69,17 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
+  // The tile's 16 loads of 1 KB, spread evenly over kDmaWaves waves.
+  constexpr int kDmaWaves = kWaves >= 4 ? 4 : kWaves >= 2 ? 2 : 1;
+  constexpr int kPerWave = 16 / kDmaWaves;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int waves = blockDim.x >> 6;  // = query heads per KV head
+  const int group = n_heads / n_kv_heads;
   const int kvh = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, r = lane & 15;
-  const int h = kvh * waves + wave;
+  const int h0 = kvh * group + kHeadsPerWave * wave;       // this wave's first head
+  const int nh = min(kHeadsPerWave, group - kHeadsPerWave * wave);  // 1 or 2 (uniform)
   const int kv_dim = n_kv_heads * 64;
   const int pos0 = __builtin_amdgcn_readfirstlane(row_pos[0]);
   const int seq = __builtin_amdgcn_readfirstlane(row_seq[0]);
@@ -82,29 +92,51 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   };
   auto valid = [&](const int id) { return id >= 0 && id < num_pages; };
 
-  // DMA of tile `tile` into buffer `buf`: 8 K loads then 8 V loads of 1 KB
-  // (8 key rows of 128 bytes each), load i issued by wave i % waves. Lane l of a
-  // load moves key row 8u + l/8, LDS slot l % 8 (the DMA lands lane l at base +
-  // 16 l), fetching the global piece that the row's swizzle maps to that slot.
-  auto issue = [&](const int tile, const int buf, const int id0, const int id1, const int id2,
-                   const int id3) {
-    for (int i = wave; i < 16; i += waves) {
-      const bool is_v = i >= 8;
-      const int u = i & 7;
-      const int row = 8 * u + (lane >> 3), slot = lane & 7;
-      const int piece = is_v ? slot ^ (2 * ((row >> 1) & 3)) : slot ^ ((row >> 1) & 7);
-      const int pj = u >> 1;
-      const int id = pj == 0 ? id0 : pj == 1 ? id1 : pj == 2 ? id2 : id3;
-      const int page = valid(id) ? id : 0;
-      const uint16_t* src = (is_v ? v_pool : k_pool) +
-                            (size_t(page) * IE_HIP_PAGE_SIZE + (row & 15)) * kv_dim + kvh * 64 +
-                            8 * piece;
-      __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1)))*)(src),
-          (void __attribute__((address_space(3)))*)(smem + buf * kBufBytes +
-                                                    (is_v ? kTileBytes : 0) + u * 1024),
-          16, 0, 0);
+  // DMA of a tile into buffer `buf`: 8 K loads and 8 V loads of 1 KB (8 key rows
+  // of 128 bytes each), the same kPerWave for every tile, so a wave can wait for
+  // "all but the newest tiles" by count. Load u (rows 8u .. 8u+7) lands lane l at
+  // base + 16 l: key row 8u + l/8, LDS slot l % 8, holding the global piece the
+  // row's swizzle maps to that slot (K: piece ^ (row/2 % 8); V: piece ^ 2*(row/2 % 4)).
+  // Per-lane byte offsets (row & 15 = 8 (u & 1) + l / 8) depend only on u & 1.
+  const int row_bytes = kv_dim * 2;
+  const int lrow = lane >> 3, lslot = lane & 7;
+  int koff[2], voff[2];
+#pragma unroll
+  for (int odd = 0; odd < 2; ++odd) {
+    const int row15 = 8 * odd + lrow;
+    koff[odd] = row15 * row_bytes + 16 * (lslot ^ (4 * odd + (lrow >> 1)));
+    voff[odd] = row15 * row_bytes + 16 * (lslot ^ (2 * (lrow >> 1)));
+  }
+  const char* kbase_g = reinterpret_cast<const char*>(k_pool) + kvh * 128;
+  const char* vbase_g = reinterpret_cast<const char*>(v_pool) + kvh * 128;
+  const size_t page_bytes = size_t(IE_HIP_PAGE_SIZE) * row_bytes;
+  auto issue = [&](const int buf, const int id0, const int id1, const int id2, const int id3) {
+    if (wave >= kDmaWaves) return;
+    // Quarter qt of the loads: qt = 0, 1 the K rows 0-31, 32-63; qt = 2, 3 the V rows.
+#pragma unroll
+    for (int k = 0; k < 4 / kDmaWaves; ++k) {
+      const int qt = wave + k * kDmaWaves;
+      const bool is_v = qt >= 2;
+      const int half = qt & 1;  // rows 32 half .. 32 half + 31: pages 2 half, 2 half + 1
+      const int ida = half ? id2 : id0, idb = half ? id3 : id1;
+      const char* base = is_v ? vbase_g : kbase_g;
+      const char* pa = base + size_t(valid(ida) ? ida : 0) * page_bytes;
+      const char* pb = base + size_t(valid(idb) ? idb : 0) * page_bytes;
+      unsigned char* dst = smem + buf * kBufBytes + (is_v ? kTileBytes : 0) + half * 4096;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {  // u = 4 half + j: page u / 2 of the tile
+        const int off = is_v ? voff[j & 1] : koff[j & 1];
+        __builtin_amdgcn_global_load_lds(
+            (const void __attribute__((address_space(1)))*)(((j >> 1) ? pb : pa) + off),
+            (void __attribute__((address_space(3)))*)(dst + j * 1024), 16, 0, 0);
+      }
     }
+  };
+  // Wait until this wave's loads of all but the newest `newer` tiles have landed.
+  auto wait_tiles = [&](const int newer) {
+    if (newer >= 2) wait_vmcnt<2 * kPerWave>();
+    else if (newer == 1) wait_vmcnt<kPerWave>();
+    else wait_vmcnt<0>();
   };
 
   for (int pass = 0; pass < 2; ++pass) {
@@ -117,19 +149,21 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     const int min_pos = pos0 + t0;      // first row's position
     const int n_tiles = max_pos / kKeys + 1;
 
-    // Query of row t0 + r, head h, as the B operand (dims 32 ks + 8g .. +8).
+    // Queries of row t0 + r for the wave's heads, times log2(e)/8, split hi + lo:
+    // the B operands of S^T (dims 32 ks + 8g .. +8).
     const int t = t0 + r;
     const bool row_ok = t < T;
     const int rp = pos0 + t;  // this lane's row position
-    op qhi[2], qlo[2];
-    {
+    op qhi[kHeadsPerWave][2], qlo[kHeadsPerWave][2];
+#pragma unroll
+    for (int hh = 0; hh < kHeadsPerWave; ++hh) {
       float4 a[2][2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         a[ks][0] = a[ks][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (row_ok) {
-          const float4* src =
-              reinterpret_cast<const float4*>(q + (size_t(t) * n_heads + h) * 64 + 32 * ks + 8 * g);
+        if (row_ok && hh < nh) {
+          const float4* src = reinterpret_cast<const float4*>(
+              q + (size_t(t) * n_heads + h0 + hh) * 64 + 32 * ks + 8 * g);
           a[ks][0] = src[0];
           a[ks][1] = src[1];
         }
@@ -143,107 +177,145 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
         for (int j = 0; j < 8; ++j) {
           E hv, lv;
           split16(x[j] * qs, hv, lv);
-          qhi[ks][j] = hv;
-          qlo[ks][j] = lv;
+          qhi[hh][ks][j] = hv;
+          qlo[hh][ks][j] = lv;
         }
       }
     }
 
-    float m = -INFINITY, l = 0.0f;  // running max (base 2), this lane's part of the sum
-    f32x4 o[4];                     // O^T: lane (g, r) holds row r, dims 16 mt + 4g + e
+    // Per head: running max (base 2), this lane's part of the sum, and O^T
+    // (lane (g, r) holds row r, dims 16 mt + 4g + e).
+    float m[kHeadsPerWave], l[kHeadsPerWave];
+    f32x4 o[kHeadsPerWave][4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+      m[hh] = -INFINITY;
+      l[hh] = 0.0f;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) o[hh][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
-    int ids[4] = {page_id(0, 0), page_id(0, 1), page_id(0, 2), page_id(0, 3)};
-    issue(0, 0, ids[0], ids[1], ids[2], ids[3]);
-    int nx[4] = {page_id(1, 0), page_id(1, 1), page_id(1, 2), page_id(1, 3)};
-    __builtin_amdgcn_s_waitcnt(0);
+    // Ring of kRing tile buffers: tiles 0 .. kRing-2 are issued up front; at
+    // iteration kb tile kb + kRing - 1 goes into the buffer tile kb - 1 used.
+    // Page ids are read one tile ahead of their DMA; `okq` queues 4 "page inside
+    // the pool" bits per tile in flight (tile kb in the lowest 4).
+    int nx[4] = {page_id(0, 0), page_id(0, 1), page_id(0, 2), page_id(0, 3)};
+    auto ok_bits = [&]() {
+      return int(valid(nx[0])) | int(valid(nx[1])) << 1 | int(valid(nx[2])) << 2 |
+             int(valid(nx[3])) << 3;
+    };
+    int okq = 0;
+    for (int pre = 0; pre < kRing - 1 && pre < n_tiles; ++pre) {
+      okq |= ok_bits() << (4 * pre);
+      issue(pre, nx[0], nx[1], nx[2], nx[3]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) nx[j] = page_id(pre + 1, j);
+    }
+    wait_tiles(min(kRing - 2, n_tiles - 1));  // tile 0 has landed
     __syncthreads();
 
     for (int kb = 0; kb < n_tiles; ++kb) {
-      const int buf = kb & 1;
-      const bool ok_pg[4] = {valid(ids[0]), valid(ids[1]), valid(ids[2]), valid(ids[3])};
-      if (kb + 1 < n_tiles) {  // the next tile into the other buffer (free since the last barrier)
-        issue(kb + 1, buf ^ 1, nx[0], nx[1], nx[2], nx[3]);
+      const int buf = kb % kRing;
+      const int okb = okq & 15;
+      okq >>= 4;
+      const int ahead = kb + kRing - 1;
+      if (ahead < n_tiles) {  // its buffer held tile kb - 1: free since the last barrier
+        okq |= ok_bits() << (4 * (kRing - 2));
+        issue(ahead % kRing, nx[0], nx[1], nx[2], nx[3]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          ids[j] = nx[j];
-          nx[j] = page_id(kb + 2, j);
-        }
+        for (int j = 0; j < 4; ++j) nx[j] = page_id(ahead + 1, j);
       }
       const int kbase = kb * kKeys;
       const unsigned char* kt = smem + buf * kBufBytes;
-      const unsigned char* vt = kt + kTileBytes;
-      const bool pages_ok = ok_pg[0] && ok_pg[1] && ok_pg[2] && ok_pg[3];
+      unsigned char* vt = smem + buf * kBufBytes + kTileBytes;
       // Keys past max_pos (the last tile) or in pages outside the pool: zero
       // their V rows before any wave reads the tile (uniform decision).
-      if (kbase + kKeys - 1 > max_pos || !pages_ok) {
-        for (int i = tid; i < kKeys * 8; i += blockDim.x) {
+      if (kbase + kKeys - 1 > max_pos || okb != 15) {
+        for (int i = tid; i < kKeys * 8; i += 64 * kWaves) {
           const int key = i >> 3;
-          if (kbase + key > max_pos || !ok_pg[key >> 4])
-            *reinterpret_cast<uint4*>(const_cast<unsigned char*>(vt) + key * 128 + (i & 7) * 16) =
-                make_uint4(0, 0, 0, 0);
+          if (kbase + key > max_pos || !((okb >> (key >> 4)) & 1))
+            *reinterpret_cast<uint4*>(vt + key * 128 + (i & 7) * 16) = make_uint4(0, 0, 0, 0);
         }
         __syncthreads();
       }
 
-      // S^T for the tile's 4 key groups of 16: A = K rows 16 kt4 + r, dims 32 ks + 8g.
-      f32x4 s[4];
+      // S^T for the tile's 4 key groups of 16, both heads: A = K rows 16 kt4 + r,
+      // dims 32 ks + 8g (read once for the two heads).
+      op ka[4][2];
 #pragma unroll
       for (int kt4 = 0; kt4 < 4; ++kt4) {
-        s[kt4] = f32x4{0.f, 0.f, 0.f, 0.f};
         const int row = 16 * kt4 + r;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const int slot = (4 * ks + g) ^ ((row >> 1) & 7);
-          const op a = *reinterpret_cast<const op*>(kt + row * 128 + slot * 16);
-          s[kt4] = M::mma(a, qhi[ks], s[kt4]);
-          s[kt4] = M::mma(a, qlo[ks], s[kt4]);
-        }
+        for (int ks = 0; ks < 2; ++ks)
+          ka[kt4][ks] = *reinterpret_cast<const op*>(kt + row * 128 +
+                                                     16 * ((4 * ks + g) ^ ((row >> 1) & 7)));
       }
+      f32x4 s[kHeadsPerWave][4];
+#pragma unroll
+      for (int kt4 = 0; kt4 < 4; ++kt4)
+#pragma unroll
+        for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            acc = M::mma(ka[kt4][ks], qhi[hh][ks], acc);
+            acc = M::mma(ka[kt4][ks], qlo[hh][ks], acc);
+          }
+          s[hh][kt4] = acc;
+        }
       // Causal mask (and masked pages) where the tile is not entirely visible.
-      if (kbase + kKeys - 1 > min_pos || !pages_ok) {
+      if (kbase + kKeys - 1 > min_pos || okb != 15) {
 #pragma unroll
         for (int kt4 = 0; kt4 < 4; ++kt4)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int kp = kbase + 16 * kt4 + 4 * g + e;
-            s[kt4][e] = (kp <= rp && ok_pg[kt4]) ? s[kt4][e] : -INFINITY;
+            const bool vis = kp <= rp && ((okb >> kt4) & 1);
+#pragma unroll
+            for (int hh = 0; hh < kHeadsPerWave; ++hh)
+              s[hh][kt4][e] = vis ? s[hh][kt4][e] : -INFINITY;
           }
       }
-      float mx = -INFINITY;
+      // Online softmax per head; P^T operands per 32-key group kg: slots 0-3 =
+      // keys 32kg + 4g + e (group 2kg), slots 4-7 = keys 32kg + 16 + 4g + e.
+      op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
 #pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4)
-        mx = fmaxf(mx, fmaxf(fmaxf(s[kt4][0], s[kt4][1]), fmaxf(s[kt4][2], s[kt4][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m, mx);
-      const float mref = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet: weights 0
-      const float corr = exp2f(m - mref);                     // m = -inf: 0
-      l *= corr;
+      for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+        float mx = -INFINITY;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) o[mt] *= corr;
-      m = m_new;
-      // P^T operands per 32-key group kg: slots 0-3 = keys 32kg + 4g + e (group
-      // 2kg), slots 4-7 = keys 32kg + 16 + 4g + e (group 2kg+1).
-      op phi[2], plo[2];
+        for (int kt4 = 0; kt4 < 4; ++kt4)
+          mx = fmaxf(mx, fmaxf(fmaxf(s[hh][kt4][0], s[hh][kt4][1]),
+                               fmaxf(s[hh][kt4][2], s[hh][kt4][3])));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m[hh], mx);
+        const float mref = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet: weights 0
+        const float corr = exp2_weight(m[hh] - mref);          // m = -inf: 0
+        float sum = 0.0f;
 #pragma unroll
-      for (int kg = 0; kg < 2; ++kg)
+        for (int kg = 0; kg < 2; ++kg)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pa = exp2f(s[2 * kg][e] - mref), pb = exp2f(s[2 * kg + 1][e] - mref);
-          l += pa + pb;
-          E ha, la, hb, lb;
-          split16(pa, ha, la);
-          split16(pb, hb, lb);
-          phi[kg][e] = ha;
-          plo[kg][e] = la;
-          phi[kg][4 + e] = hb;
-          plo[kg][4 + e] = lb;
-        }
+          for (int e = 0; e < 4; ++e) {
+            const float pa = exp2_weight(s[hh][2 * kg][e] - mref);
+            const float pb = exp2_weight(s[hh][2 * kg + 1][e] - mref);
+            sum += pa + pb;
+            E ha, la, hb, lb;
+            split16(pa, ha, la);
+            split16(pb, hb, lb);
+            phi[hh][kg][e] = ha;
+            plo[hh][kg][e] = la;
+            phi[hh][kg][4 + e] = hb;
+            plo[hh][kg][4 + e] = lb;
+          }
+        l[hh] = __builtin_fmaf(l[hh], corr, sum);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
+        m[hh] = m_new;
+      }
       // O^T += V^T P^T. Lane L reads tile row 32kg + 4g + L/4 (and +16), dims
       // 16 mt + 4 (L%4) .. +3: after the transpose lane r holds dim 16 mt + r of
-      // keys 32kg + 4g + e and 32kg + 16 + 4g + e -- P^T's slots.
+      // keys 32kg + 4g + e and 32kg + 16 + 4g + e -- P^T's slots. Each V^T operand
+      // feeds both heads.
       const int rbyte = (r & 1) * 8;
 #pragma unroll
       for (int kg = 0; kg < 2; ++kg) {
@@ -255,23 +327,64 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
           const s16x4 lo4 = lds_read_tr16(vt + vrow * 128 + slot * 16 + rbyte);
           const s16x4 hi4 = lds_read_tr16(vt + (vrow + 16) * 128 + slot * 16 + rbyte);
           const op a = join_tr<op>(lo4, hi4);
-          o[mt] = M::mma(a, phi[kg], o[mt]);
-          o[mt] = M::mma(a, plo[kg], o[mt]);
+#pragma unroll
+          for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+            o[hh][mt] = M::mma(a, phi[hh][kg], o[hh][mt]);
+            o[hh][mt] = M::mma(a, plo[hh][kg], o[hh][mt]);
+          }
         }
       }
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA of the next tile has landed
-      __syncthreads();                // every wave's DMA landed, every wave done with `buf`
+      // This wave's loads of tile kb + 1 have landed (tiles kb + 2 .. kb + kRing - 1
+      // may still be in flight); after the barrier every wave's have, and every
+      // wave is done with `buf`.
+      wait_tiles(max(0, min(kRing - 2, n_tiles - kb - 2)));
+      __syncthreads();
     }
 
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
     if (row_ok) {
-      const float il = 1.0f / l;
-      float* dst = out + (size_t(t) * n_heads + h) * 64 + 4 * g;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<f32x4*>(dst + 16 * mt) = o[mt] * il;
+      for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+        if (hh >= nh) break;
+        float lt = l[hh];
+        lt += __shfl_xor(lt, 16, 64);
+        lt += __shfl_xor(lt, 32, 64);
+        const float il = 1.0f / lt;
+        float* dst = out + (size_t(t) * n_heads + h0 + hh) * 64 + 4 * g;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<f32x4*>(dst + 16 * mt) = o[hh][mt] * il;
+      }
     }
   }
+}
+
+template <int KV>
+int launch_prefill_mfma(float* out, const float* q, const uint16_t* kp, const uint16_t* vp, int T,
+                        const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                        int n_heads, int n_kv_heads, hipStream_t stream) {
+  const int group = n_heads / n_kv_heads;
+  const int waves = (group + kHeadsPerWave - 1) / kHeadsPerWave;
+  const int n_blocks = (T + kRows - 1) / kRows;
+  const dim3 grid((n_blocks + 1) / 2, n_kv_heads), block(64 * waves);
+#define IE_PF_CASE(W)                                                                             \
+  case W:                                                                                         \
+    hipLaunchKernelGGL((prefill_mfma_kernel<KV, W>), grid, block, kLdsBytes, stream, out, q, kp, \
+                       vp, T, row_pos, row_seq, kv.tables, kv.max_pages, kv.num_pages, n_heads,   \
+                       n_kv_heads, n_blocks);                                                     \
+    break;
+  switch (waves) {
+    IE_PF_CASE(1)
+    IE_PF_CASE(2)
+    IE_PF_CASE(3)
+    IE_PF_CASE(4)
+    IE_PF_CASE(5)
+    IE_PF_CASE(6)
+    IE_PF_CASE(7)
+    IE_PF_CASE(8)
+    default:
+      return fail(IE_HIP_EINVAL, "attention_prefill: at most 8 query heads per KV head");
+  }
+#undef IE_PF_CASE
+  return check_launch("attention_prefill_mfma");
 }
 
 }  // namespace
@@ -289,20 +402,13 @@ int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const vo
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) & 15)
     return fail(IE_HIP_EINVAL, "attention_prefill: q, out and the pools must be 16-byte aligned");
-  const int group = n_heads / n_kv_heads;
-  const int n_blocks = (T + kRows - 1) / kRows;
-  const dim3 grid((n_blocks + 1) / 2, n_kv_heads), block(64 * group);
   const uint16_t* kp = static_cast<const uint16_t*>(k_pool);
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
   if (kv.kv_dtype == IE_KV_F16)
-    hipLaunchKernelGGL(prefill_mfma_kernel<IE_KV_F16>, grid, block, kLdsBytes, stream, out, q, kp,
-                       vp, T, row_pos, row_seq, kv.tables, kv.max_pages, kv.num_pages, n_heads,
-                       n_kv_heads, n_blocks);
-  else
-    hipLaunchKernelGGL(prefill_mfma_kernel<IE_KV_BF16>, grid, block, kLdsBytes, stream, out, q, kp,
-                       vp, T, row_pos, row_seq, kv.tables, kv.max_pages, kv.num_pages, n_heads,
-                       n_kv_heads, n_blocks);
-  return check_launch("attention_prefill_mfma");
+    return launch_prefill_mfma<IE_KV_F16>(out, q, kp, vp, T, row_pos, row_seq, kv, n_heads,
+                                          n_kv_heads, stream);
+  return launch_prefill_mfma<IE_KV_BF16>(out, q, kp, vp, T, row_pos, row_seq, kv, n_heads,
+                                         n_kv_heads, stream);
 }
 
 }  // namespace iehip
