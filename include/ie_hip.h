@@ -124,9 +124,10 @@ int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype);
 int ie_hip_attention_chunks(int context_tokens, int chunk_tokens);
 
 /* Bytes of workspace ie_hip_attention needs for T rows and num_chunks chunks
- * (the reference's part_o + part_ml scratch, src/cuda/kernels.cuh:82-83, plus
- * one counter per row). Allocate it once and zero-fill it once; every call
- * leaves it ready for the next. Calls that overlap on one workspace race. */
+ * (the reference's part_o + part_ml scratch, src/cuda/kernels.cuh:82-83).
+ * Allocate it once, 16-byte aligned; it needs no initialisation, since a call
+ * reads only the partials it wrote itself. Calls that overlap on one
+ * workspace race. */
 size_t ie_hip_attention_workspace_bytes(int T, int n_heads, int head_dim, int num_chunks);
 
 int ie_hip_attention(float* out, const float* q, const void* k_pool, const void* v_pool, int T,

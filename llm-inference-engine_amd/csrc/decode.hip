@@ -210,79 +210,117 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
   }
 }
 
-// One workgroup per (head, row), one lane per output dim, and as many waves as
-// it takes to give each wave at most 32 of the row's chunks (up to 16 waves):
-// wave w takes chunks w, w + W, w + 2W, ... Each lane first reads the row's
-// position (its chunk count), then loads its wave's partials -- up to 32
-// chunks, all in flight at once -- and combines them:
-//   M = max m_c, L = sum l_c e^(m_c - M), acc = sum o_c e^(m_c - M);
-// longer rows take further batches with the running (M, L, acc) rescaled. The
-// waves' (M, L, acc) are combined the same way through LDS: out = acc / L.
-constexpr int kMergeBatch = 32;
+// Split-K merge: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M), M = max m_c.
+// A workgroup takes one (head, row) and a slice of 64/S output dims (S = 1, 2
+// or 4 slices, more slices when rows x heads alone would leave compute units
+// idle). In a wave, lane = (chunk lane, dim quad): the slice's D/4 quads of
+// float4 side by side, and 64/(D/4) chunk lanes, so one load instruction
+// covers several chunks' slices. Chunk lane i of wave w takes the row's chunks
+// i + w*CL, i + (w + W)*CL, ..., kMergeBatch of them in flight at a time,
+// each folded into a running (M, L, acc) in natural-log units. The chunk
+// lanes are then combined by xor-shuffles and the waves through LDS with the
+// same rule: (M1, L1, A1) + (M2, L2, A2) = (M, L1 e^(M1-M) + L2 e^(M2-M), ...).
+constexpr int kMergeBatch = 8;
 constexpr int kMergeMaxWaves = 16;
 
-template <int HD>
-__global__ void __launch_bounds__(HD * kMergeMaxWaves)
+struct MergeAcc {
+  float m, l;
+  float4 a;
+};
+
+__device__ __forceinline__ MergeAcc merge_pair(const MergeAcc& x, const MergeAcc& y) {
+  const float m = fmaxf(x.m, y.m);
+  if (m == -INFINITY) return x;  // neither side has seen a position
+  const float ex = x.m == -INFINITY ? 0.0f : expf(x.m - m);
+  const float ey = y.m == -INFINITY ? 0.0f : expf(y.m - m);
+  MergeAcc r;
+  r.m = m;
+  r.l = __builtin_fmaf(x.l, ex, y.l * ey);
+  r.a.x = __builtin_fmaf(x.a.x, ex, y.a.x * ey);
+  r.a.y = __builtin_fmaf(x.a.y, ex, y.a.y * ey);
+  r.a.z = __builtin_fmaf(x.a.z, ex, y.a.z * ey);
+  r.a.w = __builtin_fmaf(x.a.w, ex, y.a.w * ey);
+  return r;
+}
+
+__device__ __forceinline__ MergeAcc shfl_xor_acc(const MergeAcc& x, int off) {
+  MergeAcc r;
+  r.m = __shfl_xor(x.m, off, 64);
+  r.l = __shfl_xor(x.l, off, 64);
+  r.a.x = __shfl_xor(x.a.x, off, 64);
+  r.a.y = __shfl_xor(x.a.y, off, 64);
+  r.a.z = __shfl_xor(x.a.z, off, 64);
+  r.a.w = __shfl_xor(x.a.w, off, 64);
+  return r;
+}
+
+// Q = dim quads per slice (16, 8 or 4 for S = 1, 2, 4); blockIdx = (head, row, slice).
+template <int Q>
+__global__ void __launch_bounds__(64 * kMergeMaxWaves)
 decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
                     const float* __restrict__ part_ml, const int32_t* __restrict__ row_pos,
                     int n_heads, int num_chunks, int chunk_tokens) {
-  __shared__ float red_m[kMergeMaxWaves], red_l[kMergeMaxWaves];
-  __shared__ float red_a[kMergeMaxWaves][HD];
-  const int h = blockIdx.x, t = blockIdx.y;
-  const int d = threadIdx.x % HD, w = threadIdx.x / HD, W = blockDim.x / HD;
+  constexpr int HD = 64, CL = 64 / Q;
+  __shared__ MergeAcc red[kMergeMaxWaves][Q];
+  const int h = blockIdx.x, t = blockIdx.y, s = blockIdx.z;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
+  const int qd = lane % Q, cl = lane / Q;
   const int p = row_pos[t];
   if (p < 0) return;
   const int nc = min(p / chunk_tokens + 1, num_chunks);
   if (nc <= 1) return;  // written by the partial kernel
   const size_t base = (size_t(t) * n_heads + h) * num_chunks;
+  const int dim = s * 4 * Q + 4 * qd;
   const float2* ml = reinterpret_cast<const float2*>(part_ml) + base;
-  float M = -INFINITY, L = 0.0f, acc = 0.0f;
-  for (int c0 = w; c0 < nc; c0 += kMergeBatch * W) {
+  const float4* po = reinterpret_cast<const float4*>(part_o + base * HD + dim);
+  MergeAcc acc{-INFINITY, 0.0f, make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
+  const int stride = W * CL;
+  for (int c0 = w * CL + cl; c0 < nc; c0 += kMergeBatch * stride) {
     float2 mlc[kMergeBatch];
-    float oc[kMergeBatch];
+    float4 oc[kMergeBatch];
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j) {
-      const int c = c0 + j * W;
+      const int c = c0 + j * stride;
       const bool ok = c < nc;
       mlc[j] = ok ? ml[c] : make_float2(-INFINITY, 0.0f);
-      oc[j] = ok ? part_o[(base + c) * HD + d] : 0.0f;
+      oc[j] = ok ? po[size_t(c) * (HD / 4)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    float mb = M;
+    float mb = acc.m;
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j) mb = fmaxf(mb, mlc[j].x);
     if (mb == -INFINITY) continue;  // no visible position yet
-    const float sc = M == -INFINITY ? 0.0f : expf(M - mb);
-    L *= sc;
-    acc *= sc;
+    const float sc = acc.m == -INFINITY ? 0.0f : expf(acc.m - mb);
+    acc.l *= sc;
+    acc.a.x *= sc;
+    acc.a.y *= sc;
+    acc.a.z *= sc;
+    acc.a.w *= sc;
 #pragma unroll
     for (int j = 0; j < kMergeBatch; ++j) {
-      const float e = c0 + j * W < nc ? expf(mlc[j].x - mb) : 0.0f;
-      L = __builtin_fmaf(mlc[j].y, e, L);
-      acc = __builtin_fmaf(oc[j], e, acc);
+      const float e = mlc[j].x == -INFINITY ? 0.0f : expf(mlc[j].x - mb);
+      acc.l = __builtin_fmaf(mlc[j].y, e, acc.l);
+      acc.a.x = __builtin_fmaf(oc[j].x, e, acc.a.x);
+      acc.a.y = __builtin_fmaf(oc[j].y, e, acc.a.y);
+      acc.a.z = __builtin_fmaf(oc[j].z, e, acc.a.z);
+      acc.a.w = __builtin_fmaf(oc[j].w, e, acc.a.w);
     }
-    M = mb;
+    acc.m = mb;
   }
-  const size_t o = (size_t(t) * n_heads + h) * HD + d;
+#pragma unroll
+  for (int off = Q; off < 64; off <<= 1) acc = merge_pair(acc, shfl_xor_acc(acc, off));
+  float4* dst = reinterpret_cast<float4*>(out + (size_t(t) * n_heads + h) * HD + dim);
   if (W == 1) {
-    out[o] = acc / L;
+    if (cl == 0) {
+      *dst = make_float4(acc.a.x / acc.l, acc.a.y / acc.l, acc.a.z / acc.l, acc.a.w / acc.l);
+    }
     return;
   }
-  if (d == 0) {
-    red_m[w] = M;
-    red_l[w] = L;
-  }
-  red_a[w][d] = acc;
+  if (cl == 0) red[w][qd] = acc;
   __syncthreads();
-  if (w != 0) return;
-  float mx = -INFINITY;
-  for (int i = 0; i < W; ++i) mx = fmaxf(mx, red_m[i]);
-  float lt = 0.0f, at = 0.0f;
-  for (int i = 0; i < W; ++i) {
-    const float e = red_m[i] == -INFINITY ? 0.0f : expf(red_m[i] - mx);
-    lt = __builtin_fmaf(red_l[i], e, lt);
-    at = __builtin_fmaf(red_a[i][d], e, at);
-  }
-  out[o] = at / lt;
+  if (w != 0 || cl != 0) return;
+  MergeAcc r = red[0][qd];
+  for (int i = 1; i < W; ++i) r = merge_pair(r, red[i][qd]);
+  *dst = make_float4(r.a.x / r.l, r.a.y / r.l, r.a.z / r.l, r.a.w / r.l);
 }
 
 template <int KV, int G>
@@ -331,10 +369,30 @@ int dispatch_group(int group, float* out, const float* q, const void* k_pool, co
 int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T, int n_heads,
                  int num_chunks, int chunk_tokens, hipStream_t stream) {
   if (num_chunks <= 1) return IE_HIP_OK;
-  const int waves =
-      std::min(kMergeMaxWaves, std::max(1, (num_chunks + kMergeBatch - 1) / kMergeBatch));
-  hipLaunchKernelGGL((decode_merge_kernel<64>), dim3(n_heads, T), dim3(64 * waves), 0, stream, out,
-                     ws.part_o, ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
+  // Dim slices: enough (head, row, slice) workgroups to reach every compute unit
+  // when rows x heads alone cannot (long-context batches of a few rows).
+  const int64_t pairs = int64_t(T) * n_heads;
+  const int cus = device_compute_units();
+  const int slices = pairs >= cus ? 1 : (2 * pairs >= cus ? 2 : 4);
+  const int quads = 16 / slices, chunk_lanes = 64 / quads;
+  // Waves: up to kMergeBatch chunks per lane in one pass over the longest row.
+  const int per_wave = chunk_lanes * kMergeBatch;
+  const int waves = std::min(kMergeMaxWaves, std::max(1, (num_chunks + per_wave - 1) / per_wave));
+  const dim3 grid(n_heads, T, slices), block(64 * waves);
+  switch (slices) {
+    case 1:
+      hipLaunchKernelGGL((decode_merge_kernel<16>), grid, block, 0, stream, out, ws.part_o,
+                         ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
+      break;
+    case 2:
+      hipLaunchKernelGGL((decode_merge_kernel<8>), grid, block, 0, stream, out, ws.part_o,
+                         ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_merge_kernel<4>), grid, block, 0, stream, out, ws.part_o,
+                         ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
+      break;
+  }
   return check_launch("attention_merge");
 }
 
@@ -345,15 +403,12 @@ Workspace carve_workspace(void* base, int T, int n_heads, int head_dim, int num_
   ws.part_o = reinterpret_cast<float*>(p);
   p += align256(slots * head_dim * sizeof(float));
   ws.part_ml = reinterpret_cast<float*>(p);
-  p += align256(slots * 2 * sizeof(float));
-  ws.counters = reinterpret_cast<int32_t*>(p);
   return ws;
 }
 
 size_t workspace_bytes(int T, int n_heads, int head_dim, int num_chunks) {
   const size_t slots = size_t(T) * n_heads * num_chunks;
-  return align256(slots * head_dim * sizeof(float)) + align256(slots * 2 * sizeof(float)) +
-         align256(size_t(T) * sizeof(int32_t));
+  return align256(slots * head_dim * sizeof(float)) + align256(slots * 2 * sizeof(float));
 }
 
 int device_compute_units() {
@@ -406,10 +461,13 @@ int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
   const int64_t rows = std::max(T, 1);
   const int ctx = std::max(max_context, 1);
   if (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) {
-    // Matrix-core kernel: one-wave workgroups streaming 128 positions each fill
-    // the device best (measured on MI355X); 64 when that leaves fewer than two
-    // workgroups per compute unit.
-    return rows * ie_hip_attention_chunks(ctx, 128) >= 2 * cus ? 128 : 64;
+    // Matrix-core kernel (measured on MI355X): 128-position chunks when that
+    // gives two workgroups per compute unit (one wave streams the chunk). With
+    // fewer rows, 128-position chunks still when 64-position ones would give two
+    // per unit: the kernel then splits each chunk over four waves of one page
+    // pair each, and the merge reads half the partials. 64 below that.
+    if (rows * ie_hip_attention_chunks(ctx, 128) >= 2 * cus) return 128;
+    return rows * ie_hip_attention_chunks(ctx, 64) >= 2 * cus ? 128 : 64;
   }
   // float32 VALU kernel: the largest chunk that still gives every compute unit
   // a workgroup.
@@ -438,6 +496,8 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
   if (T == 0) return IE_HIP_OK;
   if (!out || !q || !k_pool || !v_pool || !row_pos || !row_seq || !workspace)
     return fail(IE_HIP_EINVAL, "attention: null pointer");
+  if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(workspace)) & 15)
+    return fail(IE_HIP_EINVAL, "attention: out and the workspace must be 16-byte aligned");
   const int impl = attention_impl();
   if (impl != IE_HIP_IMPL_VALU &&
       decode_mfma_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens))

@@ -14,7 +14,6 @@ inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 struct Workspace {
   float* part_o = nullptr;     // [T][n_heads][num_chunks][head_dim] unnormalised partial outputs
   float* part_ml = nullptr;    // [T][n_heads][num_chunks][2] partial max and sum of exp
-  int32_t* counters = nullptr; // [T] finished-chunk counters (zero between calls)
 };
 
 Workspace carve_workspace(void* base, int T, int n_heads, int head_dim, int num_chunks);

@@ -26,7 +26,8 @@
 //
 // Layout of the work:
 //   One workgroup per non-empty (row, chunk) pair, with one wave per 128
-//   positions of the chunk (decode_mfma_waves); each wave streams its positions
+//   positions of the chunk, or per 32 when the grid is small
+//   (decode_mfma_waves); each wave streams its positions
 //   as page pairs (32 tokens, 2 pages), keeping the next pair's loads in flight
 //   while it computes the current one. The 1-D grid is numbered row by row over
 //   the chunks each row actually has (a prefix sum of the rows' chunk counts,
@@ -412,11 +413,16 @@ bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_d
          chunk_tokens <= 1024;
 }
 
-// Waves per workgroup for a chunk: about one wave per 128 positions (a wave
-// streams its positions as page pairs, one pair in flight while it computes the
-// previous one), at most 8, and a whole number of page pairs per wave.
-static int decode_mfma_waves(int chunk_tokens) {
-  int w = std::max(1, std::min(kMaxWaves, chunk_tokens / 128));
+// Waves per workgroup for a chunk. A wave streams its positions as page pairs,
+// one pair in flight while it computes the previous one, so a long stream per
+// wave hides latency when the grid is large; about one wave per 128 positions
+// then. When the grid gives fewer than two workgroups per compute unit, chunks
+// of four or more pairs take one wave per pair instead: every pair is in
+// flight at once. At most 8 waves, a whole number of pairs each.
+static int decode_mfma_waves(int chunk_tokens, int64_t slots) {
+  const bool small_grid = slots < 2 * int64_t(device_compute_units());
+  const int per_wave = small_grid && chunk_tokens >= 128 ? 32 : 128;
+  int w = std::max(1, std::min(kMaxWaves, chunk_tokens / per_wave));
   while (w > 1 && chunk_tokens % (32 * w) != 0) --w;
   return w;
 }
@@ -426,9 +432,9 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
                 hipStream_t stream) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
-  const int waves = decode_mfma_waves(chunk_tokens);
-  const size_t lds = size_t(waves) * kTile;
   const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
+  const int waves = decode_mfma_waves(chunk_tokens, slots);
+  const size_t lds = size_t(waves) * kTile;
   if (slots * n_heads * 64 * 4 > 0x7fffffff)
     return fail(IE_HIP_EINVAL, "attention: split-K workspace above 2 GB (too many rows x chunks)");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |

@@ -174,6 +174,45 @@ def test_config3_full_size(ie, O, dev, kv, impl):
     check(O, got, want, kvt, "config 3")
 
 
+@pytest.mark.parametrize("rows", [1, 12, 24])
+@pytest.mark.parametrize("kv", list(KVS))
+def test_merge_layouts(ie, O, dev, rows, kv, impl):
+    """Every split-K merge layout: rows x heads below, near and above the compute-unit
+    count (4, 2 and 1 dim slices per (head, row)) with 64-token chunks over contexts up to
+    8,192 (128 chunks: one merge wave up to four), mixed with rows that fit one chunk."""
+    rng = np.random.default_rng(100 + rows)
+    lens = [8192] + [int(x) for x in rng.integers(1, 8193, rows - 1)]
+    if rows > 2:
+        lens[1], lens[2] = 64, 65  # one chunk exactly; one position into a second chunk
+    kvt = KVS[kv]
+    tables, max_pages, num_pages = make_tables(lens, rng)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_pos = np.array([n - 1 for n in lens], np.int32)
+    row_seq = np.arange(rows, dtype=np.int32)
+    q = normal(rng, (rows, QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
+                             threads=8)
+    got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, 64)
+    check(O, got, want, kvt, f"rows {rows}")
+
+
+def test_config4_full_size(ie, O, dev):
+    """BASELINE config 4's attention: batch 1, context 32,768, bf16 KV, shuffled 16-token
+    pages, with the library's own chunk choice (512 chunks of 64 tokens)."""
+    rng = np.random.default_rng(20263)
+    kvt = KVS["bf16"]
+    L = 32768
+    tables, max_pages, num_pages = make_tables([L], rng)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_pos, row_seq = np.array([L - 1], np.int32), np.zeros(1, np.int32)
+    q = normal(rng, (1, QD))
+    ct = ie.attention_chunk_tokens(1, L, ie.KV_BF16)
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
+                             threads=8)
+    got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct)
+    check(O, got, want, kvt, f"config 4, chunk {ct}")
+
+
 @pytest.mark.parametrize("kv", ["f16", "bf16"])
 def test_mfma_forced_and_shape_limits(ie, O, dev, kv):
     """IMPL_MFMA runs the matrix-core kernel; shapes it cannot take fail loudly (no silent fallback)."""
