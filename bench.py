@@ -310,7 +310,8 @@ def bench_long(args, torch, ie, O):
                    "kv_dtype": kv, "chunk_tokens": ct, "num_chunks": nc, "seed": args.seed},
         "tok_per_s": round(1 / (ms * 1e-3), 1), "us_per_layer": round(ms * 1e3 / layers, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("long")},
         "algorithmic_bytes_per_step": nbytes,
     }
 
