@@ -129,7 +129,8 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   using op = typename M::op;
   using E = typename M::elem;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int tid = threadIdx.x, wave = kOneWave ? 0 : tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = kOneWave ? 0 : __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, r = lane & 15;
   int t, c, p, seq;
   if (!locate_chunk(blockIdx.x, T, row_pos, row_seq, num_chunks, chunk_tokens, lane, t, c, p, seq))
@@ -143,6 +144,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   const int nw = min(max(n - wt0, 0), tw);          // positions this wave attends to
   const int np = (nw + 31) >> 5;                    // its page pairs
   unsigned char* warea = smem + size_t(wave) * kTile;
+  const unsigned warea_lds = lds_address(smem) + wave * kTile;
 
   // Page id of the wave's page `pw` (uniform, scalar load); -1 past the wave's
   // positions or the table row.
@@ -186,16 +188,14 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
       for (int ks = 0; ks < 4; ++ks) ka[h][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
     }
     __builtin_amdgcn_sched_barrier(0);
-    unsigned char* tile = warea + (j & 1) * kPair;
+    const unsigned tile = warea_lds + (j & 1) * kPair;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int tok = 4 * u + g;
       const int piece = r ^ (2 * (tok & 7));
       const uint16_t* src = v_pool +
           (size_t((u >> 2) ? pb : pa) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece;
-      __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1)))*)(src),
-          (void __attribute__((address_space(3)))*)(tile + u * 1024), 16, 0, 0);
+      dma16(src, tile + u * 1024);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -277,8 +277,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     }
     float mx = fmaxf(fmaxf(fmaxf(sa[0], sa[1]), fmaxf(sa[2], sa[3])),
                      fmaxf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3])));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = group_max4(mx);
     const float m_new = fmaxf(m, mx);
     const float mref = m_new == -INFINITY ? 0.0f : m_new;  // all masked so far: weights 0
     op phi, plo;
@@ -340,8 +339,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
       o[mt] = M::mma(a, plo, o[mt]);
     }
   }
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  l = group_sum4(l);
 
   // 3. Head r's 64 output dims: tiles 4 kv_r .. 4 kv_r + 3 (its own KV head),
   //    lane group g holding dims 16 j + 4g .. +3 of tile j.

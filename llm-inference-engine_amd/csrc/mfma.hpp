@@ -46,6 +46,58 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// LDS byte address of a pointer into an LDS object.
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+  return static_cast<unsigned>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
+}
+
+// Global -> LDS DMA of 16 bytes per lane (global_load_lds_dwordx4): lane l's
+// 16 bytes at `src` land at LDS byte address `lds` + 16 l (lds uniform, in M0;
+// one wait state between the M0 write and the load). Written as inline
+// assembly so that the compiler sees no LDS store here: after the builtin form
+// it puts a vmcnt(0) before every later LDS read it cannot prove disjoint from
+// the DMA (the transposing reads among them), which stalls on every load still
+// in flight, prefetches included. Callers wait for completion themselves:
+// wait_vmcnt on the issuing wave, then a barrier where other waves read the data.
+__device__ __forceinline__ void dma16(const void* src, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+// Max and sum over the 4 lane groups of a 16-column tile (lanes r, r+16, r+32,
+// r+48), on gfx950's VALU lane swaps instead of LDS-routed shuffles. With the
+// same value in both registers, v_permlane32_swap leaves each lane holding its
+// own value and lane^32's (one in each register); v_permlane16_swap likewise
+// for lane^16. Written as inline assembly: this toolchain's builtins for these
+// two-result instructions return the first register's value for both results.
+// One wait state between a VALU write of the operands and the swap (s_nop 1,
+// as the compiler itself places before these instructions).
+__device__ __forceinline__ void lane_pair32(float x, float& a, float& b) {
+  a = x;
+  b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void lane_pair16(float x, float& a, float& b) {
+  a = x;
+  b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float group_max4(float x) {
+  float a, b;
+  lane_pair32(x, a, b);
+  lane_pair16(fmaxf(a, b), a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float group_sum4(float x) {
+  float a, b;
+  lane_pair32(x, a, b);
+  lane_pair16(a + b, a, b);
+  return a + b;
+}
+
 // Transposing LDS read (ds_read_b64_tr_b16): in each 16-lane group, lane 4a+b
 // receives element b of the 8-byte reads of lanes a, a+4, a+8, a+12.
 __device__ __forceinline__ s16x4 lds_read_tr16(const unsigned char* p) {
@@ -67,6 +119,29 @@ template <typename E>
 __device__ __forceinline__ void split16(float x, E& hi, E& lo) {
   hi = static_cast<E>(x);
   lo = static_cast<E>(__builtin_fmaf(-1.0f, static_cast<float>(hi), x));
+}
+
+// Two values split into hi + lo halves at once, for operand slots 2i, 2i+1: the hi
+// pair is one packed conversion rounding toward zero (f16: v_cvt_pkrtz), so
+// |x - hi| < 1 ulp and |x - hi - lo| ~ 2^-21 |x|; lo = x - hi, rounded to nearest.
+template <typename E>
+__device__ __forceinline__ void split16x2(float x0, float x1, E& h0, E& h1, E& l0, E& l1);
+
+template <>
+__device__ __forceinline__ void split16x2<_Float16>(float x0, float x1, _Float16& h0,
+                                                    _Float16& h1, _Float16& l0, _Float16& l1) {
+  const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+  h0 = static_cast<_Float16>(h[0]);
+  h1 = static_cast<_Float16>(h[1]);
+  l0 = static_cast<_Float16>(__builtin_fmaf(-1.0f, static_cast<float>(h[0]), x0));
+  l1 = static_cast<_Float16>(__builtin_fmaf(-1.0f, static_cast<float>(h[1]), x1));
+}
+
+template <>
+__device__ __forceinline__ void split16x2<__bf16>(float x0, float x1, __bf16& h0, __bf16& h1,
+                                                  __bf16& l0, __bf16& l1) {
+  split16(x0, h0, l0);
+  split16(x1, h1, l1);
 }
 
 // 2^x for the softmax weights: the bare v_exp_f32 (x <= 0 here; results below

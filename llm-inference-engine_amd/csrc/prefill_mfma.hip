@@ -56,6 +56,7 @@ constexpr int kLdsBytes = kRing * kBufBytes;
 constexpr int kMaxGroup = 8;
 constexpr int kHeadsPerWave = 1;           // query heads per wave (2 measured slower: fewer waves)
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyMax = 8.0f;           // log2 headroom of the lazily raised softmax max
 
 // kWaves = group / kHeadsPerWave waves (rounded up), wave w taking query heads
 // kHeadsPerWave * w .. of the KV head.
@@ -107,6 +108,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     koff[odd] = row15 * row_bytes + 16 * (lslot ^ (4 * odd + (lrow >> 1)));
     voff[odd] = row15 * row_bytes + 16 * (lslot ^ (2 * (lrow >> 1)));
   }
+  const unsigned smem_lds = lds_address(smem);
   const char* kbase_g = reinterpret_cast<const char*>(k_pool) + kvh * 128;
   const char* vbase_g = reinterpret_cast<const char*>(v_pool) + kvh * 128;
   const size_t page_bytes = size_t(IE_HIP_PAGE_SIZE) * row_bytes;
@@ -122,13 +124,11 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       const char* base = is_v ? vbase_g : kbase_g;
       const char* pa = base + size_t(valid(ida) ? ida : 0) * page_bytes;
       const char* pb = base + size_t(valid(idb) ? idb : 0) * page_bytes;
-      unsigned char* dst = smem + buf * kBufBytes + (is_v ? kTileBytes : 0) + half * 4096;
+      const unsigned dst = smem_lds + buf * kBufBytes + (is_v ? kTileBytes : 0) + half * 4096;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {  // u = 4 half + j: page u / 2 of the tile
         const int off = is_v ? voff[j & 1] : koff[j & 1];
-        __builtin_amdgcn_global_load_lds(
-            (const void __attribute__((address_space(1)))*)(((j >> 1) ? pb : pa) + off),
-            (void __attribute__((address_space(3)))*)(dst + j * 1024), 16, 0, 0);
+        dma16(((j >> 1) ? pb : pa) + off, dst + j * 1024);
       }
     }
   };
@@ -278,6 +278,10 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       }
       // Online softmax per head; P^T operands per 32-key group kg: slots 0-3 =
       // keys 32kg + 4g + e (group 2kg), slots 4-7 = keys 32kg + 16 + 4g + e.
+      // The reference max m is raised lazily: weights are 2^(s - m) with m the
+      // row's max when it was last raised, and O and l are rescaled only when some
+      // row of the wave sees its max grow past m + kLazyMax (so weights stay below
+      // 2^kLazyMax, which the 16-bit hi + lo split carries at full precision).
       op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
 #pragma unroll
       for (int hh = 0; hh < kHeadsPerWave; ++hh) {
@@ -286,31 +290,40 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
         for (int kt4 = 0; kt4 < 4; ++kt4)
           mx = fmaxf(mx, fmaxf(fmaxf(s[hh][kt4][0], s[hh][kt4][1]),
                                fmaxf(s[hh][kt4][2], s[hh][kt4][3])));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m[hh], mx);
-        const float mref = m_new == -INFINITY ? 0.0f : m_new;  // nothing visible yet: weights 0
-        const float corr = exp2_weight(m[hh] - mref);          // m = -inf: 0
+        mx = group_max4(mx);
+        // m = -inf (nothing visible yet) always counts as growth when mx is finite.
+        if (__builtin_amdgcn_ballot_w64(mx > m[hh] + kLazyMax) != 0) {
+          const float m_new = fmaxf(m[hh], mx);
+          const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m[hh] - m_new);  // m = -inf: 0
+          l[hh] *= corr;
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
+          m[hh] = m_new;
+        }
+        const float mref = m[hh] == -INFINITY ? 0.0f : m[hh];  // nothing visible yet: weights 0
         float sum = 0.0f;
 #pragma unroll
         for (int kg = 0; kg < 2; ++kg)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float pa = exp2_weight(s[hh][2 * kg][e] - mref);
-            const float pb = exp2_weight(s[hh][2 * kg + 1][e] - mref);
-            sum += pa + pb;
-            E ha, la, hb, lb;
-            split16(pa, ha, la);
-            split16(pb, hb, lb);
-            phi[hh][kg][e] = ha;
-            plo[hh][kg][e] = la;
-            phi[hh][kg][4 + e] = hb;
-            plo[hh][kg][4 + e] = lb;
+          for (int e = 0; e < 4; e += 2) {
+            const float pa0 = exp2_weight(s[hh][2 * kg][e] - mref);
+            const float pa1 = exp2_weight(s[hh][2 * kg][e + 1] - mref);
+            const float pb0 = exp2_weight(s[hh][2 * kg + 1][e] - mref);
+            const float pb1 = exp2_weight(s[hh][2 * kg + 1][e + 1] - mref);
+            sum += (pa0 + pa1) + (pb0 + pb1);
+            E h0, h1, l0, l1;
+            split16x2(pa0, pa1, h0, h1, l0, l1);
+            phi[hh][kg][e] = h0;
+            phi[hh][kg][e + 1] = h1;
+            plo[hh][kg][e] = l0;
+            plo[hh][kg][e + 1] = l1;
+            split16x2(pb0, pb1, h0, h1, l0, l1);
+            phi[hh][kg][4 + e] = h0;
+            phi[hh][kg][5 + e] = h1;
+            plo[hh][kg][4 + e] = l0;
+            plo[hh][kg][5 + e] = l1;
           }
-        l[hh] = __builtin_fmaf(l[hh], corr, sum);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
-        m[hh] = m_new;
+        l[hh] += sum;
       }
       // O^T += V^T P^T. Lane L reads tile row 32kg + 4g + L/4 (and +16), dims
       // 16 mt + 4 (L%4) .. +3: after the transpose lane r holds dim 16 mt + r of
@@ -346,8 +359,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       for (int hh = 0; hh < kHeadsPerWave; ++hh) {
         if (hh >= nh) break;
         float lt = l[hh];
-        lt += __shfl_xor(lt, 16, 64);
-        lt += __shfl_xor(lt, 32, 64);
+        lt = group_sum4(lt);
         const float il = 1.0f / lt;
         float* dst = out + (size_t(t) * n_heads + h0 + hh) * 64 + 4 * g;
 #pragma unroll
