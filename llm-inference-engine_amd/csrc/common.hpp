@@ -19,6 +19,8 @@ void clear_error();
 int fail(int code, const std::string& msg);
 // Turns a failed HIP call or launch into IE_HIP_ELAUNCH with a message.
 int check_hip(hipError_t err, const char* what);
+// Compute units of the current device (256 on MI355X; the fallback when the query fails).
+int device_compute_units();
 int check_launch(const char* kernel);
 
 // -------------------------------------------------------- KV conversions ---

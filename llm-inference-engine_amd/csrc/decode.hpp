@@ -18,7 +18,6 @@ struct Workspace {
 
 Workspace carve_workspace(void* base, int T, int n_heads, int head_dim, int num_chunks);
 size_t workspace_bytes(int T, int n_heads, int head_dim, int num_chunks);
-int device_compute_units();
 
 int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T, int n_heads,
                  int num_chunks, int chunk_tokens, hipStream_t stream);

@@ -51,17 +51,18 @@ constexpr int kRows = 16;                  // query rows per block (one MFMA col
 constexpr int kKeys = 64;                  // keys per LDS tile
 constexpr int kTileBytes = kKeys * 128;    // 64 keys x 64 dims x 2 B
 constexpr int kBufBytes = 2 * kTileBytes;  // K tile + V tile
-constexpr int kRing = 4;                   // tiles in LDS: one computed, three in flight
-constexpr int kLdsBytes = kRing * kBufBytes;
 constexpr int kMaxGroup = 8;
 constexpr int kHeadsPerWave = 1;           // query heads per wave (2 measured slower: fewer waves)
+static_assert(kHeadsPerWave == 1, "the team exchange hands over one head per wave");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;           // log2 headroom of the lazily raised softmax max
 
-// kWaves = group / kHeadsPerWave waves (rounded up), wave w taking query heads
-// kHeadsPerWave * w .. of the KV head.
-template <int KV, int kWaves>
-__global__ void __launch_bounds__(64 * kWaves)
+// kWaves = group / kHeadsPerWave waves per team (rounded up), wave w of a team
+// taking query heads kHeadsPerWave * w .. of the KV head. kTeams teams of
+// kWaves waves split each block's key tiles (team t takes tiles kTeams s + t)
+// and merge their (m, l, O) through LDS at the end of the block.
+template <int KV, int kWaves, int kTeams>
+__global__ void __launch_bounds__(64 * kWaves * kTeams)
 prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
                     const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
                     int T, const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
@@ -70,14 +71,19 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
-  // The tile's 16 loads of 1 KB, spread evenly over kDmaWaves waves.
+  constexpr int kRingSteps = kTeams == 1 ? 4 : 3;  // steps of kTeams tiles in LDS
+  op ones;  // all-ones A operand: row sums of P^T on the matrix cores
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = static_cast<E>(1.0f);
+  // A tile's 16 loads of 1 KB, spread evenly over kDmaWaves waves of its team.
   constexpr int kDmaWaves = kWaves >= 4 ? 4 : kWaves >= 2 ? 2 : 1;
   constexpr int kPerWave = 16 / kDmaWaves;
   extern __shared__ __align__(16) unsigned char smem[];
   const int group = n_heads / n_kv_heads;
   const int kvh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int team = wave_id / kWaves, wave = wave_id - team * kWaves;
   const int g = lane >> 4, r = lane & 15;
   const int h0 = kvh * group + kHeadsPerWave * wave;       // this wave's first head
   const int nh = min(kHeadsPerWave, group - kHeadsPerWave * wave);  // 1 or 2 (uniform)
@@ -92,10 +98,12 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     return pi < max_pages ? tab[pi] : -1;
   };
   auto valid = [&](const int id) { return id >= 0 && id < num_pages; };
+  // Buffer of the tile a team takes at step s.
+  auto buffer = [&](const int ring_step, const int tm) { return ring_step * kTeams + tm; };
 
   // DMA of a tile into buffer `buf`: 8 K loads and 8 V loads of 1 KB (8 key rows
   // of 128 bytes each), the same kPerWave for every tile, so a wave can wait for
-  // "all but the newest tiles" by count. Load u (rows 8u .. 8u+7) lands lane l at
+  // "all but the newest steps" by count. Load u (rows 8u .. 8u+7) lands lane l at
   // base + 16 l: key row 8u + l/8, LDS slot l % 8, holding the global piece the
   // row's swizzle maps to that slot (K: piece ^ (row/2 % 8); V: piece ^ 2*(row/2 % 4)).
   // Per-lane byte offsets (row & 15 = 8 (u & 1) + l / 8) depend only on u & 1.
@@ -112,7 +120,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   const char* kbase_g = reinterpret_cast<const char*>(k_pool) + kvh * 128;
   const char* vbase_g = reinterpret_cast<const char*>(v_pool) + kvh * 128;
   const size_t page_bytes = size_t(IE_HIP_PAGE_SIZE) * row_bytes;
-  auto issue = [&](const int buf, const int id0, const int id1, const int id2, const int id3) {
+  auto issue = [&](const int buf, const int* id) {
     if (wave >= kDmaWaves) return;
     // Quarter qt of the loads: qt = 0, 1 the K rows 0-31, 32-63; qt = 2, 3 the V rows.
 #pragma unroll
@@ -120,7 +128,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       const int qt = wave + k * kDmaWaves;
       const bool is_v = qt >= 2;
       const int half = qt & 1;  // rows 32 half .. 32 half + 31: pages 2 half, 2 half + 1
-      const int ida = half ? id2 : id0, idb = half ? id3 : id1;
+      const int ida = half ? id[2] : id[0], idb = half ? id[3] : id[1];
       const char* base = is_v ? vbase_g : kbase_g;
       const char* pa = base + size_t(valid(ida) ? ida : 0) * page_bytes;
       const char* pb = base + size_t(valid(idb) ? idb : 0) * page_bytes;
@@ -132,8 +140,8 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       }
     }
   };
-  // Wait until this wave's loads of all but the newest `newer` tiles have landed.
-  auto wait_tiles = [&](const int newer) {
+  // Wait until this wave's loads of all but the newest `newer` steps have landed.
+  auto wait_steps = [&](const int newer) {
     if (newer >= 2) wait_vmcnt<2 * kPerWave>();
     else if (newer == 1) wait_vmcnt<kPerWave>();
     else wait_vmcnt<0>();
@@ -148,6 +156,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     const int max_pos = pos0 + t_last;  // last position any row of the block sees
     const int min_pos = pos0 + t0;      // first row's position
     const int n_tiles = max_pos / kKeys + 1;
+    const int n_steps = (n_tiles + kTeams - 1) / kTeams;
 
     // Queries of row t0 + r for the wave's heads, times log2(e)/8, split hi + lo:
     // the B operands of S^T (dims 32 ks + 8g .. +8).
@@ -183,190 +192,300 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       }
     }
 
-    // Per head: running max (base 2), this lane's part of the sum, and O^T
+    // Per head: running max (base 2), the row's sum of weights, and O^T
     // (lane (g, r) holds row r, dims 16 mt + 4g + e).
-    float m[kHeadsPerWave], l[kHeadsPerWave];
+    float m[kHeadsPerWave];
+    f32x4 lacc[kHeadsPerWave];  // every entry: the row's sum of weights
     f32x4 o[kHeadsPerWave][4];
 #pragma unroll
     for (int hh = 0; hh < kHeadsPerWave; ++hh) {
       m[hh] = -INFINITY;
-      l[hh] = 0.0f;
+      lacc[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) o[hh][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // Ring of kRing tile buffers: tiles 0 .. kRing-2 are issued up front; at
-    // iteration kb tile kb + kRing - 1 goes into the buffer tile kb - 1 used.
-    // Page ids are read one tile ahead of their DMA; `okq` queues 4 "page inside
-    // the pool" bits per tile in flight (tile kb in the lowest 4).
-    int nx[4] = {page_id(0, 0), page_id(0, 1), page_id(0, 2), page_id(0, 3)};
-    auto ok_bits = [&]() {
-      return int(valid(nx[0])) | int(valid(nx[1])) << 1 | int(valid(nx[2])) << 2 |
-             int(valid(nx[3])) << 3;
-    };
-    int okq = 0;
-    for (int pre = 0; pre < kRing - 1 && pre < n_tiles; ++pre) {
-      okq |= ok_bits() << (4 * pre);
-      issue(pre, nx[0], nx[1], nx[2], nx[3]);
+    // Ring of kRingSteps steps of kTeams tile buffers: steps 0 .. kRingSteps-2
+    // are issued up front; at step s, step s + kRingSteps - 1 goes into the
+    // buffers step s - 1 used. Every wave reads the page ids of every tile of a
+    // step (one step ahead of its DMA): `okq` queues 4 "page inside the pool"
+    // bits per tile in flight (step s's tiles in the lowest 4 kTeams bits), so
+    // that the zeroing decision below is the same in every wave. A step past the
+    // last tile still loads (in-pool pages, never read), keeping every step's
+    // load count the same for the counted waits.
+    constexpr int kStepBits = 4 * kTeams;
+    int nx[kTeams][4];
+    auto read_ids = [&](const int step) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) nx[j] = page_id(pre + 1, j);
+      for (int tm = 0; tm < kTeams; ++tm)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) nx[tm][j] = page_id(kTeams * step + tm, j);
+    };
+    // This team's tile ids of the step held in nx (selected, not indexed by the
+    // run-time team, which would put nx in scratch memory).
+    auto mine = [&](int (&id)[4]) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) id[j] = (kTeams == 1 || team == 0) ? nx[0][j] : nx[kTeams - 1][j];
+    };
+    auto ok_bits = [&]() {
+      int b = 0;
+#pragma unroll
+      for (int tm = 0; tm < kTeams; ++tm)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b |= int(valid(nx[tm][j])) << (4 * tm + j);
+      return b;
+    };
+    read_ids(0);
+    int okq = 0;
+    for (int pre = 0; pre < kRingSteps - 1 && pre < n_steps; ++pre) {
+      okq |= ok_bits() << (kStepBits * pre);
+      int id[4];
+      mine(id);
+      issue(buffer(pre, team), id);
+      read_ids(pre + 1);
     }
-    wait_tiles(min(kRing - 2, n_tiles - 1));  // tile 0 has landed
+    wait_steps(min(kRingSteps - 2, n_steps - 1));  // step 0 has landed
     __syncthreads();
 
-    for (int kb = 0; kb < n_tiles; ++kb) {
-      const int buf = kb % kRing;
-      const int okb = okq & 15;
-      okq >>= 4;
-      const int ahead = kb + kRing - 1;
-      if (ahead < n_tiles) {  // its buffer held tile kb - 1: free since the last barrier
-        okq |= ok_bits() << (4 * (kRing - 2));
-        issue(ahead % kRing, nx[0], nx[1], nx[2], nx[3]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) nx[j] = page_id(ahead + 1, j);
+    int rs = 0;                    // ring slot of step s
+    int is = kRingSteps - 1;       // ring slot of step s + kRingSteps - 1
+    for (int st = 0; st < n_steps; ++st) {
+      const int oks = okq & ((1 << kStepBits) - 1);
+      okq >>= kStepBits;
+      const int ahead = st + kRingSteps - 1;
+      if (ahead < n_steps) {  // its buffers held step s - 1: free since the last barrier
+        okq |= ok_bits() << (kStepBits * (kRingSteps - 2));
+        int id[4];
+        mine(id);
+        issue(buffer(is, team), id);
+        read_ids(ahead + 1);
       }
+      is = is + 1 == kRingSteps ? 0 : is + 1;
+      const int kb = kTeams * st + team;  // this team's tile
+      const int okb = (oks >> (4 * team)) & 15;
+      const int buf = buffer(rs, team);
+      rs = rs + 1 == kRingSteps ? 0 : rs + 1;
       const int kbase = kb * kKeys;
       const unsigned char* kt = smem + buf * kBufBytes;
       unsigned char* vt = smem + buf * kBufBytes + kTileBytes;
       // Keys past max_pos (the last tile) or in pages outside the pool: zero
-      // their V rows before any wave reads the tile (uniform decision).
-      if (kbase + kKeys - 1 > max_pos || okb != 15) {
-        for (int i = tid; i < kKeys * 8; i += 64 * kWaves) {
-          const int key = i >> 3;
-          if (kbase + key > max_pos || !((okb >> (key >> 4)) & 1))
-            *reinterpret_cast<uint4*>(vt + key * 128 + (i & 7) * 16) = make_uint4(0, 0, 0, 0);
+      // their V rows before the team reads the tile. The decision covers every
+      // tile of the step, so every wave takes the same branch and barrier.
+      bool zero_step = false;
+#pragma unroll
+      for (int tm = 0; tm < kTeams; ++tm) {
+        const int tile = kTeams * st + tm;
+        zero_step |= tile < n_tiles &&
+                     (tile * kKeys + kKeys - 1 > max_pos || ((oks >> (4 * tm)) & 15) != 15);
+      }
+      if (zero_step) {
+        if (kb < n_tiles) {
+          for (int i = tid - 64 * kWaves * team; i < kKeys * 8; i += 64 * kWaves) {
+            const int key = i >> 3;
+            if (kbase + key > max_pos || !((okb >> (key >> 4)) & 1))
+              *reinterpret_cast<uint4*>(vt + key * 128 + (i & 7) * 16) = make_uint4(0, 0, 0, 0);
+          }
         }
         __syncthreads();
       }
 
-      // S^T for the tile's 4 key groups of 16, both heads: A = K rows 16 kt4 + r,
-      // dims 32 ks + 8g (read once for the two heads).
-      op ka[4][2];
+      if (kb < n_tiles) {  // uniform per team (the odd last step of team 1 skips)
+        // S^T for the tile's 4 key groups of 16: A = K rows 16 kt4 + r, dims 32 ks + 8g.
+        op ka[4][2];
 #pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4) {
-        const int row = 16 * kt4 + r;
+        for (int kt4 = 0; kt4 < 4; ++kt4) {
+          const int row = 16 * kt4 + r;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          ka[kt4][ks] = *reinterpret_cast<const op*>(kt + row * 128 +
-                                                     16 * ((4 * ks + g) ^ ((row >> 1) & 7)));
-      }
-      f32x4 s[kHeadsPerWave][4];
-#pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4)
-#pragma unroll
-        for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            acc = M::mma(ka[kt4][ks], qhi[hh][ks], acc);
-            acc = M::mma(ka[kt4][ks], qlo[hh][ks], acc);
-          }
-          s[hh][kt4] = acc;
+          for (int ks = 0; ks < 2; ++ks)
+            ka[kt4][ks] = *reinterpret_cast<const op*>(kt + row * 128 +
+                                                       16 * ((4 * ks + g) ^ ((row >> 1) & 7)));
         }
-      // Causal mask (and masked pages) where the tile is not entirely visible.
-      if (kbase + kKeys - 1 > min_pos || okb != 15) {
+        // The accumulators start at -mref (the row's reference max, 0 before any
+        // visible key), so the products come out as s - mref directly.
+        float mref[kHeadsPerWave];
+#pragma unroll
+        for (int hh = 0; hh < kHeadsPerWave; ++hh) mref[hh] = m[hh] == -INFINITY ? 0.0f : m[hh];
+        f32x4 s[kHeadsPerWave][4];
 #pragma unroll
         for (int kt4 = 0; kt4 < 4; ++kt4)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int kp = kbase + 16 * kt4 + 4 * g + e;
-            const bool vis = kp <= rp && ((okb >> kt4) & 1);
-#pragma unroll
-            for (int hh = 0; hh < kHeadsPerWave; ++hh)
-              s[hh][kt4][e] = vis ? s[hh][kt4][e] : -INFINITY;
-          }
-      }
-      // Online softmax per head; P^T operands per 32-key group kg: slots 0-3 =
-      // keys 32kg + 4g + e (group 2kg), slots 4-7 = keys 32kg + 16 + 4g + e.
-      // The reference max m is raised lazily: weights are 2^(s - m) with m the
-      // row's max when it was last raised, and O and l are rescaled only when some
-      // row of the wave sees its max grow past m + kLazyMax (so weights stay below
-      // 2^kLazyMax, which the 16-bit hi + lo split carries at full precision).
-      op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
-#pragma unroll
-      for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kt4 = 0; kt4 < 4; ++kt4)
-          mx = fmaxf(mx, fmaxf(fmaxf(s[hh][kt4][0], s[hh][kt4][1]),
-                               fmaxf(s[hh][kt4][2], s[hh][kt4][3])));
-        mx = group_max4(mx);
-        // m = -inf (nothing visible yet) always counts as growth when mx is finite.
-        if (__builtin_amdgcn_ballot_w64(mx > m[hh] + kLazyMax) != 0) {
-          const float m_new = fmaxf(m[hh], mx);
-          const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m[hh] - m_new);  // m = -inf: 0
-          l[hh] *= corr;
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
-          m[hh] = m_new;
-        }
-        const float mref = m[hh] == -INFINITY ? 0.0f : m[hh];  // nothing visible yet: weights 0
-        float sum = 0.0f;
-#pragma unroll
-        for (int kg = 0; kg < 2; ++kg)
-#pragma unroll
-          for (int e = 0; e < 4; e += 2) {
-            const float pa0 = exp2_weight(s[hh][2 * kg][e] - mref);
-            const float pa1 = exp2_weight(s[hh][2 * kg][e + 1] - mref);
-            const float pb0 = exp2_weight(s[hh][2 * kg + 1][e] - mref);
-            const float pb1 = exp2_weight(s[hh][2 * kg + 1][e + 1] - mref);
-            sum += (pa0 + pa1) + (pb0 + pb1);
-            E h0, h1, l0, l1;
-            split16x2(pa0, pa1, h0, h1, l0, l1);
-            phi[hh][kg][e] = h0;
-            phi[hh][kg][e + 1] = h1;
-            plo[hh][kg][e] = l0;
-            plo[hh][kg][e + 1] = l1;
-            split16x2(pb0, pb1, h0, h1, l0, l1);
-            phi[hh][kg][4 + e] = h0;
-            phi[hh][kg][5 + e] = h1;
-            plo[hh][kg][4 + e] = l0;
-            plo[hh][kg][5 + e] = l1;
-          }
-        l[hh] += sum;
-      }
-      // O^T += V^T P^T. Lane L reads tile row 32kg + 4g + L/4 (and +16), dims
-      // 16 mt + 4 (L%4) .. +3: after the transpose lane r holds dim 16 mt + r of
-      // keys 32kg + 4g + e and 32kg + 16 + 4g + e -- P^T's slots. Each V^T operand
-      // feeds both heads.
-      const int rbyte = (r & 1) * 8;
-#pragma unroll
-      for (int kg = 0; kg < 2; ++kg) {
-        const int vrow = 32 * kg + 4 * g + (r >> 2);
-        const int sw = 2 * ((vrow >> 1) & 3);  // same for vrow + 16
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const int slot = (2 * mt + ((r >> 1) & 1)) ^ sw;
-          const s16x4 lo4 = lds_read_tr16(vt + vrow * 128 + slot * 16 + rbyte);
-          const s16x4 hi4 = lds_read_tr16(vt + (vrow + 16) * 128 + slot * 16 + rbyte);
-          const op a = join_tr<op>(lo4, hi4);
 #pragma unroll
           for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-            o[hh][mt] = M::mma(a, phi[hh][kg], o[hh][mt]);
-            o[hh][mt] = M::mma(a, plo[hh][kg], o[hh][mt]);
+            f32x4 acc = {-mref[hh], -mref[hh], -mref[hh], -mref[hh]};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              acc = M::mma(ka[kt4][ks], qhi[hh][ks], acc);
+              acc = M::mma(ka[kt4][ks], qlo[hh][ks], acc);
+            }
+            s[hh][kt4] = acc;
+          }
+        // Causal mask (and masked pages) where the tile is not entirely visible.
+        if (kbase + kKeys - 1 > min_pos || okb != 15) {
+#pragma unroll
+          for (int kt4 = 0; kt4 < 4; ++kt4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int kp = kbase + 16 * kt4 + 4 * g + e;
+              const bool vis = kp <= rp && ((okb >> kt4) & 1);
+#pragma unroll
+              for (int hh = 0; hh < kHeadsPerWave; ++hh)
+                s[hh][kt4][e] = vis ? s[hh][kt4][e] : -INFINITY;
+            }
+        }
+        // Online softmax per head on s - mref; P^T operands per 32-key group kg:
+        // slots 0-3 = keys 32kg + 4g + e (group 2kg), slots 4-7 = keys 32kg + 16 +
+        // 4g + e. The reference max m is raised lazily: weights are 2^(s - m) with
+        // m the row's max when it was last raised, and O and l are rescaled only
+        // when some row of the wave sees its max grow past m + kLazyMax (so weights
+        // stay below 2^kLazyMax, which the 16-bit hi + lo split carries at full
+        // precision). The row sums l come from the matrix cores (below).
+        op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
+#pragma unroll
+        for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int kt4 = 0; kt4 < 4; ++kt4)
+            mx = fmaxf(mx, fmaxf(fmaxf(s[hh][kt4][0], s[hh][kt4][1]),
+                                 fmaxf(s[hh][kt4][2], s[hh][kt4][3])));
+          mx = group_max4(mx);  // the tile's row max, relative to mref
+          // m = -inf (nothing visible yet) always counts as growth when mx is finite.
+          const bool grow = m[hh] == -INFINITY ? mx != -INFINITY : mx > kLazyMax;
+          if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = fmaxf(m[hh], mref[hh] + mx);
+            const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m[hh] - m_new);  // m = -inf: 0
+            lacc[hh] *= corr;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
+            m[hh] = m_new;
+            // Re-reference this tile's scores to the new max.
+            const float shift = (m_new == -INFINITY ? 0.0f : m_new) - mref[hh];
+#pragma unroll
+            for (int kt4 = 0; kt4 < 4; ++kt4) s[hh][kt4] -= shift;
+          }
+#pragma unroll
+          for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+              const float pa0 = exp2_weight(s[hh][2 * kg][e]);
+              const float pa1 = exp2_weight(s[hh][2 * kg][e + 1]);
+              const float pb0 = exp2_weight(s[hh][2 * kg + 1][e]);
+              const float pb1 = exp2_weight(s[hh][2 * kg + 1][e + 1]);
+              E h0, h1, l0, l1;
+              split16x2(pa0, pa1, h0, h1, l0, l1);
+              phi[hh][kg][e] = h0;
+              phi[hh][kg][e + 1] = h1;
+              plo[hh][kg][e] = l0;
+              plo[hh][kg][e + 1] = l1;
+              split16x2(pb0, pb1, h0, h1, l0, l1);
+              phi[hh][kg][4 + e] = h0;
+              phi[hh][kg][5 + e] = h1;
+              plo[hh][kg][4 + e] = l0;
+              plo[hh][kg][5 + e] = l1;
+            }
+          // Row sums: an all-ones A operand against P^T puts sum_k P[r][k] of the
+          // tile's 32-key group in every entry of lane r's accumulator.
+#pragma unroll
+          for (int kg = 0; kg < 2; ++kg) {
+            lacc[hh] = M::mma(ones, phi[hh][kg], lacc[hh]);
+            lacc[hh] = M::mma(ones, plo[hh][kg], lacc[hh]);
+          }
+        }
+        // O^T += V^T P^T. Lane L reads tile row 32kg + 4g + L/4 (and +16), dims
+        // 16 mt + 4 (L%4) .. +3: after the transpose lane r holds dim 16 mt + r of
+        // keys 32kg + 4g + e and 32kg + 16 + 4g + e -- P^T's slots.
+        const int rbyte = (r & 1) * 8;
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) {
+          const int vrow = 32 * kg + 4 * g + (r >> 2);
+          const int sw = 2 * ((vrow >> 1) & 3);  // same for vrow + 16
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            const int slot = (2 * mt + ((r >> 1) & 1)) ^ sw;
+            const s16x4 lo4 = lds_read_tr16(vt + vrow * 128 + slot * 16 + rbyte);
+            const s16x4 hi4 = lds_read_tr16(vt + (vrow + 16) * 128 + slot * 16 + rbyte);
+            const op a = join_tr<op>(lo4, hi4);
+#pragma unroll
+            for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+              o[hh][mt] = M::mma(a, phi[hh][kg], o[hh][mt]);
+              o[hh][mt] = M::mma(a, plo[hh][kg], o[hh][mt]);
+            }
           }
         }
       }
-      // This wave's loads of tile kb + 1 have landed (tiles kb + 2 .. kb + kRing - 1
-      // may still be in flight); after the barrier every wave's have, and every
-      // wave is done with `buf`.
-      wait_tiles(max(0, min(kRing - 2, n_tiles - kb - 2)));
+      // This wave's loads of step s + 1 have landed (later steps may still be in
+      // flight); after the barrier every wave's have, and every wave is done
+      // with step s's buffers.
+      wait_steps(max(0, min(kRingSteps - 2, n_steps - st - 2)));
       __syncthreads();
     }
 
-    if (row_ok) {
+    // Teams 1.. hand their (m, l, O) to team 0 through LDS (the ring is idle:
+    // every load has landed and every tile was consumed before the last barrier).
+    // Lane L of a head's waves holds the same rows and dims in every team.
+    float* xo = reinterpret_cast<float*>(smem);                       // [kWaves][4][64] f32x4
+    float* xml = reinterpret_cast<float*>(smem + kWaves * 4096);      // [kWaves][64] float2
+    if constexpr (kTeams > 1) {
+#pragma unroll
+      for (int tm = 1; tm < kTeams; ++tm) {
+        if (team == tm) {
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt)
+            *reinterpret_cast<f32x4*>(xo + ((wave * 4 + mt) * 64 + lane) * 4) = o[0][mt];
+          *reinterpret_cast<float2*>(xml + (wave * 64 + lane) * 2) = make_float2(m[0], lacc[0][0]);
+        }
+        __syncthreads();
+        if (team == 0) {
+          const float2 ml = *reinterpret_cast<const float2*>(xml + (wave * 64 + lane) * 2);
+          const float m_new = fmaxf(m[0], ml.x);
+          const float c0 = m[0] == -INFINITY ? 0.0f : exp2_weight(m[0] - m_new);
+          const float c1 = ml.x == -INFINITY ? 0.0f : exp2_weight(ml.x - m_new);
+          lacc[0][0] = lacc[0][0] * c0 + ml.y * c1;
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            const f32x4 o1 = *reinterpret_cast<const f32x4*>(xo + ((wave * 4 + mt) * 64 + lane) * 4);
+            o[0][mt] = o[0][mt] * c0 + o1 * c1;
+          }
+          m[0] = m_new;
+        }
+        __syncthreads();  // the exchange area is free again (next team or next pass)
+      }
+    }
+
+    if (team == 0 && row_ok) {
 #pragma unroll
       for (int hh = 0; hh < kHeadsPerWave; ++hh) {
         if (hh >= nh) break;
-        float lt = l[hh];
-        lt = group_sum4(lt);
-        const float il = 1.0f / lt;
+        const float il = 1.0f / lacc[hh][0];
         float* dst = out + (size_t(t) * n_heads + h0 + hh) * 64 + 4 * g;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<f32x4*>(dst + 16 * mt) = o[hh][mt] * il;
       }
     }
   }
+}
+
+// LDS of the kernel: the ring of steps (at least the team exchange area).
+template <int kTeams>
+constexpr int prefill_lds_bytes() {
+  return (kTeams == 1 ? 4 : 3) * kTeams * kBufBytes;
+}
+
+template <int KV, int W, int kTeams>
+int launch_prefill_variant(const dim3 grid, float* out, const float* q, const uint16_t* kp,
+                           const uint16_t* vp, int T, const int32_t* row_pos,
+                           const int32_t* row_seq, const ie_kv_layout& kv, int n_heads,
+                           int n_kv_heads, int n_blocks, hipStream_t stream) {
+  constexpr int lds = prefill_lds_bytes<kTeams>();
+  static_assert(lds >= W * 4096 + W * 512, "team exchange area must fit in the ring");
+  if (lds > 65536) {  // above the default dynamic-LDS cap, within gfx950's 160 KB
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(prefill_mfma_kernel<KV, W, kTeams>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (int rc = check_hip(attr, "hipFuncSetAttribute(attention_prefill_mfma)")) return rc;
+  }
+  hipLaunchKernelGGL((prefill_mfma_kernel<KV, W, kTeams>), grid, dim3(64 * W * kTeams), lds,
+                     stream, out, q, kp, vp, T, row_pos, row_seq, kv.tables, kv.max_pages,
+                     kv.num_pages, n_heads, n_kv_heads, n_blocks);
+  return check_launch("attention_prefill_mfma");
 }
 
 template <int KV>
@@ -376,13 +495,17 @@ int launch_prefill_mfma(float* out, const float* q, const uint16_t* kp, const ui
   const int group = n_heads / n_kv_heads;
   const int waves = (group + kHeadsPerWave - 1) / kHeadsPerWave;
   const int n_blocks = (T + kRows - 1) / kRows;
-  const dim3 grid((n_blocks + 1) / 2, n_kv_heads), block(64 * waves);
+  const dim3 grid((n_blocks + 1) / 2, n_kv_heads);
+  // Two teams splitting the key tiles when the grid alone leaves compute units
+  // without a workgroup or with one: twice the waves per CU, half the serial
+  // tile chain per wave. Larger grids already hold two workgroups per CU.
+  const bool teams2 = int64_t(grid.x) * grid.y <= device_compute_units();
 #define IE_PF_CASE(W)                                                                             \
   case W:                                                                                         \
-    hipLaunchKernelGGL((prefill_mfma_kernel<KV, W>), grid, block, kLdsBytes, stream, out, q, kp, \
-                       vp, T, row_pos, row_seq, kv.tables, kv.max_pages, kv.num_pages, n_heads,   \
-                       n_kv_heads, n_blocks);                                                     \
-    break;
+    return teams2 ? launch_prefill_variant<KV, W, 2>(grid, out, q, kp, vp, T, row_pos, row_seq,   \
+                                                      kv, n_heads, n_kv_heads, n_blocks, stream)  \
+                  : launch_prefill_variant<KV, W, 1>(grid, out, q, kp, vp, T, row_pos, row_seq,   \
+                                                      kv, n_heads, n_kv_heads, n_blocks, stream);
   switch (waves) {
     IE_PF_CASE(1)
     IE_PF_CASE(2)
@@ -396,7 +519,6 @@ int launch_prefill_mfma(float* out, const float* q, const uint16_t* kp, const ui
       return fail(IE_HIP_EINVAL, "attention_prefill: at most 8 query heads per KV head");
   }
 #undef IE_PF_CASE
-  return check_launch("attention_prefill_mfma");
 }
 
 }  // namespace
