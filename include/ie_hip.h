@@ -113,10 +113,10 @@ int ie_hip_rope_and_cache(float* q, const float* k, const float* v, void* k_pool
  * Supported: head_dim 64, n_heads/n_kv_heads <= 8 (the reference's limits at
  * this head_dim), page size 16. */
 
-/* Chunk size (tokens, a multiple of 64) for T rows of up to `max_context`
- * tokens with a KV cache of `kv_dtype`: enough chunks to fill the device's
- * compute units, sized for the kernel that dtype runs on (matrix-core kernel
- * for 16-bit caches, VALU kernel for float32). Replaces the reference's fixed
+/* Chunk size (tokens: a multiple of 64 for 16-bit caches, of 32 for float32)
+ * for T rows of up to `max_context` tokens with a KV cache of `kv_dtype`:
+ * enough chunks to fill the device's compute units, sized for the matrix-core
+ * kernel that dtype runs on. Replaces the reference's fixed
  * attention_chunks(max_seq_len) sizing (src/cuda/kernels.cu:1387-1391). */
 int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype);
 
@@ -140,8 +140,8 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
  * (row_pos[t] = row_pos[0] + t), e.g. a prompt chunk already appended with
  * ie_hip_rope_and_cache. Replaces attention_prefill_supported /
  * attention_prefill (src/cuda/kernels.cuh:89-96, kernels.cu:527-776,1350-1385).
- * f16/bf16 KV: QK^T and PV tiles on bf16 MFMA (split hi+lo operands, float32
- * accumulation). f32 KV: float32 VALU tiles. No workspace. */
+ * f16/bf16 KV: QK^T and PV tiles on MFMA in the cache's 16-bit type (split hi +
+ * lo operands, float32 accumulation). f32 KV: float32 VALU tiles. No workspace. */
 int ie_hip_attention_prefill_supported(int n_heads, int n_kv_heads, int head_dim);
 int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, const void* v_pool,
                              int T, const int32_t* row_pos, const int32_t* row_seq,

@@ -469,11 +469,13 @@ int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
     if (rows * ie_hip_attention_chunks(ctx, 128) >= 2 * cus) return 128;
     return rows * ie_hip_attention_chunks(ctx, 64) >= 2 * cus ? 128 : 64;
   }
-  // float32 VALU kernel: the largest chunk that still gives every compute unit
-  // a workgroup.
-  for (int ct : {512, 256, 128, 64})
-    if (rows * ie_hip_attention_chunks(ctx, ct) >= cus) return ct;
-  return 64;
+  // float32 (matrix-core kernel, one page in flight per wave; measured on
+  // MI355X): the largest chunk up to 256 positions that still gives two
+  // workgroups per compute unit -- long chains of pages per wave where the grid
+  // is large, short ones where few rows must fill the device.
+  for (int ct : {256, 128, 64})
+    if (rows * ie_hip_attention_chunks(ctx, ct) >= 2 * cus) return ct;
+  return 32;
 }
 
 size_t ie_hip_attention_workspace_bytes(int T, int n_heads, int head_dim, int num_chunks) {
@@ -503,10 +505,14 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
       decode_mfma_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens))
     return decode_mfma(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
                        workspace, n_heads, n_kv_heads, stream);
+  if (impl != IE_HIP_IMPL_VALU &&
+      decode_mfma_f32_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens))
+    return decode_mfma_f32(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks,
+                           chunk_tokens, workspace, n_heads, n_kv_heads, stream);
   if (impl == IE_HIP_IMPL_MFMA)
-    return fail(IE_HIP_EINVAL, "attention: the MFMA kernel does not support this shape "
-                               "(16-bit KV, kv_dim 128, n_heads <= 16, chunk a multiple of 64 "
-                               "up to 1024)");
+    return fail(IE_HIP_EINVAL, "attention: the MFMA kernels do not support this shape "
+                               "(kv_dim 128, n_heads <= 16; 16-bit KV: chunk a multiple of 64 "
+                               "up to 1024; f32 KV: a multiple of 16 up to 1024)");
   return decode_valu(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
                      workspace, n_heads, n_kv_heads, stream);
 }

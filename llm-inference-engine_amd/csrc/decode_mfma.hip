@@ -401,6 +401,187 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// float32 KV caches: the same products on v_mfma_f32_16x16x4_f32 (full fp32
+// operands, so no hi + lo split), one 16-token page at a time.
+//   S^T[16 tok x 16 heads] = K_page[16 x 128] . Qbd^T[128 x 16]: 32 steps of 4
+//     dims. The reduction order is free, so step s takes dims 32g + s for the
+//     4 lane groups g: lane (g, r) holds token r's dims 32g .. 32g+31 (128
+//     contiguous bytes, 8 16-byte loads) and, as B, head r's query at the same
+//     dims of the block-diagonal Qbd (zero outside its own KV head).
+//   O^T[128 dims x 16 heads] += V^T[128 x 16 tok] . P^T[16 tok x 16 heads]: 8
+//     tiles of 16 dims, 4 steps of 4 tokens. Step s takes tokens 4g + s, so
+//     the B operand of lane (g, r) is its own weight of token 4g + s (the S^T
+//     result it already holds). Row i of tile mt is dim 4i + mt (mt < 4) or
+//     64 + 4i + mt - 4: lane (g, r) reads dims 4r .. 4r+3 and 64 + 4r .. +3 of
+//     token 4g + s, two 16-byte LDS reads that 16 lanes take from 256
+//     contiguous bytes, and ends up holding head r's dims 16g + 4t + e of its
+//     own KV head's 64 (o[4 kv_r + e][t]).
+// K goes straight into registers; V into LDS by DMA (8 KB per page, two page
+// buffers per wave), the next page's loads in flight while the wave computes.
+// One wave per (row, chunk); the grid is numbered as for the 16-bit kernel.
+constexpr int kPageF32 = 16 * kKvd * 4;  // bytes of one f32 page of one pool
+
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+decode_partial_mfma_f32(float* __restrict__ out, float* __restrict__ part_o,
+                        float* __restrict__ part_ml, const float* __restrict__ q,
+                        const float* __restrict__ k_pool, const float* __restrict__ v_pool,
+                        const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
+                        const int32_t* __restrict__ tables, int T, int max_pages, int num_pages,
+                        int n_heads, int group, int num_chunks, int chunk_tokens) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x;
+  const int g = lane >> 4, r = lane & 15;
+  int t, c, p, seq;
+  if (!locate_chunk(blockIdx.x, T, row_pos, row_seq, num_chunks, chunk_tokens, lane, t, c, p, seq))
+    return;  // past the batch's last chunk
+  const int s0 = c * chunk_tokens;
+  const int n = min(s0 + chunk_tokens, p + 1) - s0;  // positions of this chunk
+  const bool single = s0 == 0 && p < chunk_tokens;  // the row fits this one chunk
+  const int npg = (n + IE_HIP_PAGE_SIZE - 1) / IE_HIP_PAGE_SIZE;
+  const int pi0 = s0 / IE_HIP_PAGE_SIZE;
+  const int32_t* row_tab = tables + size_t(seq) * max_pages;
+  auto page_id = [&](const int pw) -> int {
+    const int pi = pi0 + pw;
+    return (16 * pw < n && pi < max_pages) ? row_tab[pi] : -1;
+  };
+  auto valid = [&](const int id) { return id >= 0 && id < num_pages; };
+
+  // Head r's query, times log2(e)/8, at dims 32 (g & 1) .. +31 of its head when
+  // g / 2 is its KV head (the B operands of the 32 score steps), else zeros.
+  // Every lane loads (a head in range) before page 0's loads go out, and zeros
+  // what is not its own after: the loads travel together, unpredicated.
+  const bool head_ok = r < n_heads;
+  const int kv_r = r >= group;
+  const bool mine = head_ok && (g >> 1) == kv_r;
+  float4 qx[8];
+  {
+    const float4* qrow = reinterpret_cast<const float4*>(
+        q + (size_t(t) * n_heads + (head_ok ? r : 0)) * 64 + 32 * (g & 1));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qx[i] = qrow[i];
+  }
+
+  // Loads of page j: K (token r, dims 32g..+31) into `kv`, V by DMA into LDS
+  // buffer j & 1 in row-major order (load u moves tokens 2u, 2u+1; lane l's 16
+  // bytes land at base + 16 l). A page outside the pool loads page 0 and is
+  // masked in the math.
+  float4 kv[8];
+  const unsigned vbuf_lds = lds_address(smem);
+  auto issue = [&](const int j, const int pid) {
+    __builtin_amdgcn_sched_barrier(0);
+    const float4* krow =
+        reinterpret_cast<const float4*>(k_pool + (size_t(pid) * IE_HIP_PAGE_SIZE + r) * kKvd + 32 * g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kv[i] = krow[i];
+    __builtin_amdgcn_sched_barrier(0);
+    const char* vsrc = reinterpret_cast<const char*>(v_pool) + size_t(pid) * kPageF32 + 16 * lane;
+    const unsigned dst = vbuf_lds + (j & 1) * kPageF32;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) dma16(vsrc + u * 1024, dst + u * 1024);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int cur = page_id(0), nxt = page_id(1);
+  issue(0, valid(cur) ? cur : 0);  // a located chunk has at least one position
+  float qb[32];
+  {
+    const float qm = mine ? 0.125f * kLog2e : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      qb[4 * i + 0] = qx[i].x * qm;
+      qb[4 * i + 1] = qx[i].y * qm;
+      qb[4 * i + 2] = qx[i].z * qm;
+      qb[4 * i + 3] = qx[i].w * qm;
+    }
+  }
+
+  float m = -INFINITY, l = 0.0f;  // running max (base 2) and this lane's part of the sum
+  f32x4 o[8];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < npg; ++j) {
+    // S^T of page j: lane (g, r) gets tokens 4g + e of head r.
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[i].x, qb[4 * i + 0], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[i].y, qb[4 * i + 1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[i].z, qb[4 * i + 2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[i].w, qb[4 * i + 3], s, 0, 0, 0);
+    }
+    const bool ok = valid(cur);
+    const bool more = j + 1 < npg;
+    if (more) {  // page j+1: K into `kv` (just consumed), V into the other buffer
+      issue(j + 1, valid(nxt) ? nxt : 0);
+      cur = nxt;
+      nxt = page_id(j + 2);
+    }
+    const int tj = 16 * j;  // first token of the page within the chunk
+    const bool full = tj + 16 <= n && ok;
+    if (!full) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] = (ok && tj + 4 * g + e < n) ? s[e] : -INFINITY;
+    }
+    const float mx = group_max4(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+    const float m_new = fmaxf(m, mx);
+    const float mref = m_new == -INFINITY ? 0.0f : m_new;  // all masked so far: weights 0
+    float pw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pw[e] = exp2_weight(s[e] - mref);
+    const float corr = exp2_weight(m - mref);  // m = -inf (nothing seen yet): 0
+    l = __builtin_fmaf(l, corr, (pw[0] + pw[1]) + (pw[2] + pw[3]));
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) o[mt] *= corr;
+    m = m_new;
+
+    // V of page j has landed once only page j+1's 16 loads may remain.
+    if (more)
+      wait_vmcnt<16>();
+    else
+      wait_vmcnt<0>();
+    const float* vt = reinterpret_cast<const float*>(smem + (j & 1) * kPageF32);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tok = 4 * g + e;
+      float4 va = *reinterpret_cast<const float4*>(vt + tok * kKvd + 4 * r);
+      float4 vb = *reinterpret_cast<const float4*>(vt + tok * kKvd + 64 + 4 * r);
+      if (!full && !(ok && tj + tok < n)) {  // 0 * (stale inf or NaN) is not 0
+        va = make_float4(0.f, 0.f, 0.f, 0.f);
+        vb = va;
+      }
+      o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.x, pw[e], o[0], 0, 0, 0);
+      o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.y, pw[e], o[1], 0, 0, 0);
+      o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.z, pw[e], o[2], 0, 0, 0);
+      o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.w, pw[e], o[3], 0, 0, 0);
+      o[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.x, pw[e], o[4], 0, 0, 0);
+      o[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.y, pw[e], o[5], 0, 0, 0);
+      o[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.z, pw[e], o[6], 0, 0, 0);
+      o[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.w, pw[e], o[7], 0, 0, 0);
+    }
+  }
+  l = group_sum4(l);
+  if (!head_ok) return;
+  // Head r's dims 16g + 4e' .. +3 of its own KV head: o[4 kv_r + 0..3][e'].
+  const size_t head = size_t(t) * n_heads + r;
+  const int b = 4 * kv_r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const f32x4 v = {o[b][e], o[b + 1][e], o[b + 2][e], o[b + 3][e]};
+    const int d = 16 * g + 4 * e;
+    if (single) {
+      *reinterpret_cast<f32x4*>(out + head * 64 + d) = v * (1.0f / l);
+    } else {
+      const size_t slot = head * num_chunks + c;
+      *reinterpret_cast<f32x4*>(part_o + slot * 64 + d) = v;
+    }
+  }
+  if (!single && g == 0) {
+    const size_t slot = head * num_chunks + c;
+    *reinterpret_cast<float2*>(part_ml + 2 * slot) = make_float2(m * kLn2, l);
+  }
+}
+
 }  // namespace
 
 bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim,
@@ -470,6 +651,37 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
   }
 #undef IE_DECODE_LAUNCH
   if (int rc = check_launch("attention_mfma")) return rc;
+  return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
+}
+
+}  // namespace iehip
+
+namespace iehip {
+
+bool decode_mfma_f32_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim,
+                               int chunk_tokens) {
+  return kv_dtype == IE_KV_F32 && head_dim == 64 && n_kv_heads * head_dim == kKvd &&
+         n_heads <= 16 && n_heads % n_kv_heads == 0 && chunk_tokens % IE_HIP_PAGE_SIZE == 0 &&
+         chunk_tokens >= IE_HIP_PAGE_SIZE && chunk_tokens <= 1024;
+}
+
+int decode_mfma_f32(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                    const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                    int num_chunks, int chunk_tokens, void* workspace, int n_heads,
+                    int n_kv_heads, hipStream_t stream) {
+  const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
+  const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
+  if (slots * n_heads * 64 * 4 > 0x7fffffff)
+    return fail(IE_HIP_EINVAL, "attention: split-K workspace above 2 GB (too many rows x chunks)");
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_pool) |
+       reinterpret_cast<uintptr_t>(v_pool)) & 15)
+    return fail(IE_HIP_EINVAL, "attention: q, out and the pools must be 16-byte aligned");
+  hipLaunchKernelGGL(decode_partial_mfma_f32, dim3(static_cast<unsigned>(slots)), dim3(64),
+                     2 * kPageF32, stream, out, ws.part_o, ws.part_ml, q,
+                     static_cast<const float*>(k_pool), static_cast<const float*>(v_pool), row_pos,
+                     row_seq, kv.tables, T, kv.max_pages, kv.num_pages, n_heads,
+                     n_heads / n_kv_heads, num_chunks, chunk_tokens);
+  if (int rc = check_launch("attention_mfma_f32")) return rc;
   return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
 }
 
