@@ -196,7 +196,7 @@ int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, con
     return prefill_mfma_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads,
                                n_kv_heads, stream);
   if (impl == IE_HIP_IMPL_MFMA)
-    return fail(IE_HIP_EINVAL, "attention_prefill: the MFMA kernel needs a 16-bit KV cache");
+    return fail(IE_HIP_EINVAL, "attention_prefill: the MFMA kernels do not support this shape");
   return prefill_valu_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads, n_kv_heads,
                              stream);
 }

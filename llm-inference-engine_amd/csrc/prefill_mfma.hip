@@ -521,13 +521,275 @@ int launch_prefill_mfma(float* out, const float* q, const uint16_t* kp, const ui
 #undef IE_PF_CASE
 }
 
+
+// ---------------------------------------------------------------------------
+// float32 KV caches: the same block structure on v_mfma_f32_16x16x4_f32 (full
+// fp32 operands: no hi + lo split, 16x the matrix-core time per product of the
+// 16-bit kernel, still far above the VALU path).
+//   S^T[16 keys x 16 rows] per key group of 16: 16 steps of 4 dims; step s
+//     takes dims 16g + s for lane group g, so lane (g, r) reads key r's dims
+//     16g .. 16g+15 (64 bytes, 4 LDS reads) and holds, as B, row r's query at
+//     the same dims.
+//   O^T[64 dims x 16 rows] += V^T . P^T: 16 steps of 4 keys; step (kt4, s)
+//     takes keys 16 kt4 + 4g + s, so lane (g, r)'s B operand is its own score
+//     of that key; row i of tile mt is dim 4i + mt, so its A operand is the
+//     16-byte piece r of that key's V row (one LDS read, the 4 tiles' values).
+//     Lane (g, r) ends up holding row r's dims 16g + 4t + mt (o[mt][t]).
+// K/V tiles of 64 keys (16 KB each, f32) go through a ring of 3 tiles in LDS
+// by DMA. K rows are stored with their 16-byte pieces swizzled (piece ^ (key
+// & 15)), so the 16 lanes of a group reading the same dims of 16 keys hit
+// distinct banks; V rows are read a whole row per 16 lanes and stay as they are.
+constexpr int kTileF32 = kKeys * 64 * 4;     // 16 KB: one f32 K or V tile of one KV head
+constexpr int kBufF32 = 2 * kTileF32;        // K tile + V tile
+constexpr int kRingF32 = 3;
+
+template <int kWaves>
+__global__ void __launch_bounds__(64 * kWaves)
+prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
+                        const float* __restrict__ k_pool, const float* __restrict__ v_pool, int T,
+                        const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
+                        const int32_t* __restrict__ tables, int max_pages, int num_pages,
+                        int n_heads, int n_kv_heads, int n_blocks) {
+  // A tile's 32 loads of 1 KB (16 K, 16 V), spread evenly over kDmaWaves waves.
+  constexpr int kDmaWaves = kWaves >= 4 ? 4 : kWaves >= 2 ? 2 : 1;
+  constexpr int kPerWave = 32 / kDmaWaves;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int group = n_heads / n_kv_heads;
+  const int kvh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int h0 = kvh * group + wave;  // this wave's head
+  const int kv_dim = n_kv_heads * 64;
+  const int pos0 = __builtin_amdgcn_readfirstlane(row_pos[0]);
+  const int seq = __builtin_amdgcn_readfirstlane(row_seq[0]);
+  const int32_t* tab = tables + size_t(seq) * max_pages;
+  auto page_id = [&](const int tile, const int j) -> int {
+    const int pi = tile * (kKeys / IE_HIP_PAGE_SIZE) + j;
+    return pi < max_pages ? tab[pi] : -1;
+  };
+  auto valid = [&](const int id) { return id >= 0 && id < num_pages; };
+
+  // DMA of a tile into buffer `buf`: load u (0..15 K, 16..31 V) moves keys
+  // 4 (u & 15) .. +3 (page (u & 15) / 4 of the tile); lane l lands at base + 16 l:
+  // key 4 (u & 15) + l / 16, LDS slot l % 16, holding global piece slot ^ (key & 15)
+  // for K and piece slot for V.
+  const size_t row_bytes = size_t(kv_dim) * 4;
+  const int lkey = lane >> 4, lslot = lane & 15;
+  const unsigned smem_lds = lds_address(smem);
+  const char* kbase_g = reinterpret_cast<const char*>(k_pool) + kvh * 256;
+  const char* vbase_g = reinterpret_cast<const char*>(v_pool) + kvh * 256;
+  auto issue = [&](const int buf, const int id0, const int id1, const int id2, const int id3) {
+    if (wave >= kDmaWaves) return;
+#pragma unroll
+    for (int k = 0; k < kPerWave; ++k) {
+      const int u = wave * kPerWave + k;        // 0..31
+      const bool is_v = u >= 16;
+      const int uu = u & 15;
+      const int pg = uu >> 2;                   // page of the tile
+      const int id = pg == 0 ? id0 : pg == 1 ? id1 : pg == 2 ? id2 : id3;
+      const int key = 4 * uu + lkey;            // key within the tile
+      const int piece = is_v ? lslot : (lslot ^ (key & 15));
+      const char* src = (is_v ? vbase_g : kbase_g) +
+                        (size_t(valid(id) ? id : 0) * IE_HIP_PAGE_SIZE + (key & 15)) * row_bytes +
+                        16 * piece;
+      dma16(src, smem_lds + buf * kBufF32 + (is_v ? kTileF32 : 0) + uu * 1024);
+    }
+  };
+  auto wait_tiles = [&](const int newer) {
+    if (newer >= 1) wait_vmcnt<kPerWave>();
+    else wait_vmcnt<0>();
+  };
+
+  for (int pass = 0; pass < 2; ++pass) {
+    const int hi_block = n_blocks - 1 - int(blockIdx.x);
+    const int rb = pass == 0 ? hi_block : int(blockIdx.x);
+    if (pass == 1 && rb == hi_block) break;  // the middle block of an odd count
+    const int t0 = rb * kRows;
+    const int t_last = min(t0 + kRows, T) - 1;
+    const int max_pos = pos0 + t_last;
+    const int min_pos = pos0 + t0;
+    const int n_tiles = max_pos / kKeys + 1;
+    const int t = t0 + r;
+    const bool row_ok = t < T;
+    const int rp = pos0 + t;
+
+    // Row r's query, times log2(e)/8, at dims 16g .. 16g+15 (B of the score steps).
+    float qb[16];
+    {
+      const float4* src = reinterpret_cast<const float4*>(
+          q + (size_t(row_ok ? t : t0) * n_heads + h0) * 64 + 16 * g);
+      const float qs = row_ok ? 0.125f * kLog2e : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 x = src[i];
+        qb[4 * i + 0] = x.x * qs;
+        qb[4 * i + 1] = x.y * qs;
+        qb[4 * i + 2] = x.z * qs;
+        qb[4 * i + 3] = x.w * qs;
+      }
+    }
+    float m = -INFINITY, l = 0.0f;  // running max (base 2), this lane's part of the sum
+    f32x4 o[4];                      // o[mt][t]: row r, dim 16g + 4t + mt
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Ring of kRingF32 tiles; page ids read one tile ahead; okq: 4 "page inside
+    // the pool" bits per tile in flight (tile kb in the lowest 4).
+    int nx[4] = {page_id(0, 0), page_id(0, 1), page_id(0, 2), page_id(0, 3)};
+    auto ok_bits = [&]() {
+      return int(valid(nx[0])) | int(valid(nx[1])) << 1 | int(valid(nx[2])) << 2 |
+             int(valid(nx[3])) << 3;
+    };
+    int okq = 0;
+    for (int pre = 0; pre < kRingF32 - 1 && pre < n_tiles; ++pre) {
+      okq |= ok_bits() << (4 * pre);
+      issue(pre, nx[0], nx[1], nx[2], nx[3]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) nx[j] = page_id(pre + 1, j);
+    }
+    wait_tiles(min(kRingF32 - 2, n_tiles - 1));  // tile 0 has landed
+    __syncthreads();
+
+    int buf = 0, ibuf = kRingF32 - 1;
+    for (int kb = 0; kb < n_tiles; ++kb) {
+      const int okb = okq & 15;
+      okq >>= 4;
+      const int ahead = kb + kRingF32 - 1;
+      if (ahead < n_tiles) {  // its buffer held tile kb - 1: free since the last barrier
+        okq |= ok_bits() << (4 * (kRingF32 - 2));
+        issue(ibuf, nx[0], nx[1], nx[2], nx[3]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) nx[j] = page_id(ahead + 1, j);
+      }
+      ibuf = ibuf + 1 == kRingF32 ? 0 : ibuf + 1;
+      const int kbase = kb * kKeys;
+      const unsigned char* kt = smem + buf * kBufF32;
+      unsigned char* vt = smem + buf * kBufF32 + kTileF32;
+      buf = buf + 1 == kRingF32 ? 0 : buf + 1;
+      // Keys past max_pos or in pages outside the pool: zero their V rows first.
+      if (kbase + kKeys - 1 > max_pos || okb != 15) {
+        for (int i = tid; i < kKeys * 16; i += 64 * kWaves) {
+          const int key = i >> 4;
+          if (kbase + key > max_pos || !((okb >> (key >> 4)) & 1))
+            *reinterpret_cast<uint4*>(vt + key * 256 + (i & 15) * 16) = make_uint4(0, 0, 0, 0);
+        }
+        __syncthreads();
+      }
+      const float mref = m == -INFINITY ? 0.0f : m;
+      // S^T per key group kt4: A = key 16 kt4 + r, dims 16g + s.
+      f32x4 s[4];
+#pragma unroll
+      for (int kt4 = 0; kt4 < 4; ++kt4) {
+        const int key = 16 * kt4 + r;
+        float ka[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 x = *reinterpret_cast<const float4*>(kt + key * 256 +
+                                                            16 * ((4 * g + i) ^ (key & 15)));
+          ka[4 * i + 0] = x.x;
+          ka[4 * i + 1] = x.y;
+          ka[4 * i + 2] = x.z;
+          ka[4 * i + 3] = x.w;
+        }
+        f32x4 acc = {-mref, -mref, -mref, -mref};
+#pragma unroll
+        for (int st = 0; st < 16; ++st)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[st], qb[st], acc, 0, 0, 0);
+        s[kt4] = acc;
+      }
+      if (kbase + kKeys - 1 > min_pos || okb != 15) {
+#pragma unroll
+        for (int kt4 = 0; kt4 < 4; ++kt4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int kp = kbase + 16 * kt4 + 4 * g + e;
+            s[kt4][e] = (kp <= rp && ((okb >> kt4) & 1)) ? s[kt4][e] : -INFINITY;
+          }
+      }
+      // Online softmax on s - mref, the reference max raised lazily (as in the
+      // 16-bit kernel: O and l rescaled only when a row's max grows past
+      // m + kLazyMax somewhere in the wave).
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt4 = 0; kt4 < 4; ++kt4)
+        mx = fmaxf(mx, fmaxf(fmaxf(s[kt4][0], s[kt4][1]), fmaxf(s[kt4][2], s[kt4][3])));
+      mx = group_max4(mx);
+      const bool grow = m == -INFINITY ? mx != -INFINITY : mx > kLazyMax;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = fmaxf(m, mref + mx);
+        const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m - m_new);  // m = -inf: 0
+        l *= corr;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) o[mt] *= corr;
+        m = m_new;
+        const float shift = (m_new == -INFINITY ? 0.0f : m_new) - mref;
+#pragma unroll
+        for (int kt4 = 0; kt4 < 4; ++kt4) s[kt4] -= shift;
+      }
+      float sum = 0.0f;
+#pragma unroll
+      for (int kt4 = 0; kt4 < 4; ++kt4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[kt4][e] = exp2_weight(s[kt4][e]);
+          sum += s[kt4][e];
+        }
+      l += sum;
+      // O^T += V^T P^T: step (kt4, e) takes key 16 kt4 + 4g + e; lane (g, r)
+      // reads that key's V piece r (dims 4r .. 4r+3, the 4 tiles' A values).
+#pragma unroll
+      for (int kt4 = 0; kt4 < 4; ++kt4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float4 v = *reinterpret_cast<const float4*>(vt + (16 * kt4 + 4 * g + e) * 256 + 16 * r);
+          const float pw = s[kt4][e];
+          o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, pw, o[0], 0, 0, 0);
+          o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.y, pw, o[1], 0, 0, 0);
+          o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.z, pw, o[2], 0, 0, 0);
+          o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.w, pw, o[3], 0, 0, 0);
+        }
+      wait_tiles(max(0, min(kRingF32 - 2, n_tiles - kb - 2)));
+      __syncthreads();
+    }
+
+    l = group_sum4(l);
+    if (row_ok) {
+      const float il = 1.0f / l;
+      float* dst = out + (size_t(t) * n_heads + h0) * 64 + 16 * g;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f32x4 v = {o[0][e], o[1][e], o[2][e], o[3][e]};
+        *reinterpret_cast<f32x4*>(dst + 4 * e) = v * il;
+      }
+    }
+  }
+}
+
+template <int W>
+int launch_prefill_f32(const dim3 grid, float* out, const float* q, const float* kp,
+                       const float* vp, int T, const int32_t* row_pos, const int32_t* row_seq,
+                       const ie_kv_layout& kv, int n_heads, int n_kv_heads, int n_blocks,
+                       hipStream_t stream) {
+  constexpr int lds = kRingF32 * kBufF32;  // 96 KB
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(prefill_mfma_f32_kernel<W>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (int rc = check_hip(attr, "hipFuncSetAttribute(attention_prefill_mfma_f32)")) return rc;
+  hipLaunchKernelGGL((prefill_mfma_f32_kernel<W>), grid, dim3(64 * W), lds, stream, out, q, kp,
+                     vp, T, row_pos, row_seq, kv.tables, kv.max_pages, kv.num_pages, n_heads,
+                     n_kv_heads, n_blocks);
+  return check_launch("attention_prefill_mfma_f32");
+}
+
 }  // namespace
 
 bool prefill_mfma_enabled() { return true; }
 
 bool prefill_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim) {
-  return (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) && head_dim == 64 && n_kv_heads > 0 &&
-         n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= kMaxGroup;
+  return (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16 || kv_dtype == IE_KV_F32) &&
+         head_dim == 64 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 &&
+         n_heads / n_kv_heads <= kMaxGroup;
 }
 
 int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
@@ -536,6 +798,29 @@ int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const vo
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) & 15)
     return fail(IE_HIP_EINVAL, "attention_prefill: q, out and the pools must be 16-byte aligned");
+  if (kv.kv_dtype == IE_KV_F32) {
+    const int group = n_heads / n_kv_heads;
+    const int n_blocks = (T + kRows - 1) / kRows;
+    const dim3 grid((n_blocks + 1) / 2, n_kv_heads);
+    const float* kf = static_cast<const float*>(k_pool);
+    const float* vf = static_cast<const float*>(v_pool);
+    switch (group) {
+#define IE_PF32_CASE(W)                                                                      \
+  case W:                                                                                    \
+    return launch_prefill_f32<W>(grid, out, q, kf, vf, T, row_pos, row_seq, kv, n_heads,     \
+                                 n_kv_heads, n_blocks, stream);
+      IE_PF32_CASE(1)
+      IE_PF32_CASE(2)
+      IE_PF32_CASE(3)
+      IE_PF32_CASE(4)
+      IE_PF32_CASE(5)
+      IE_PF32_CASE(6)
+      IE_PF32_CASE(7)
+      IE_PF32_CASE(8)
+#undef IE_PF32_CASE
+    }
+    return fail(IE_HIP_EINVAL, "attention_prefill: at most 8 query heads per KV head");
+  }
   const uint16_t* kp = static_cast<const uint16_t*>(k_pool);
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
   if (kv.kv_dtype == IE_KV_F16)
