@@ -135,6 +135,28 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
                      int num_chunks, int chunk_tokens, void* workspace, int n_heads,
                      int n_kv_heads, int head_dim, hipStream_t stream);
 
+/* ------------------------------------------ decode step in one launch ---
+ * ie_hip_rope_and_cache followed by ie_hip_attention, in one launch: the
+ * reference's per-layer decode sequence rope_and_cache + attention
+ * (src/cuda/kernels.cuh:69-87, called at src/cuda/cuda_runner.cu:440-445),
+ * without the separate append kernel. Pages and `out` are bit-identical to the
+ * two calls; unlike them, q is not rotated in place (the rotation happens in
+ * registers; q is only read). Requires rows of distinct sequences (no row
+ * reads the position another row of the launch appends -- a decode step), a
+ * 16-bit KV cache and the matrix-core decode kernel's shapes (head_dim 64,
+ * n_kv_heads*64 == 128, n_heads <= 16, chunk_tokens a multiple of 64 up to
+ * 1024) under IE_HIP_IMPL_AUTO or _MFMA; otherwise EINVAL: use the two calls.
+ * Arguments as for those two calls; k, v, the table and the workspace must be
+ * 16-byte aligned. */
+int ie_hip_rope_cache_attention_supported(int kv_dtype, int n_heads, int n_kv_heads,
+                                          int head_dim, int chunk_tokens);
+int ie_hip_rope_cache_attention(float* out, const float* q, const float* k, const float* v,
+                                void* k_pool, void* v_pool, const float* rope_table,
+                                int table_positions, int T, const int32_t* row_pos,
+                                const int32_t* row_seq, ie_kv_layout kv, int num_chunks,
+                                int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
+                                int head_dim, hipStream_t stream);
+
 /* --------------------------------------------------- prefill attention ---
  * Attention for T rows that are consecutive positions of ONE sequence
  * (row_pos[t] = row_pos[0] + t), e.g. a prompt chunk already appended with

@@ -517,4 +517,53 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
                      workspace, n_heads, n_kv_heads, stream);
 }
 
+static bool fused_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim,
+                            int chunk_tokens) {
+  return attention_impl() != IE_HIP_IMPL_VALU &&
+         decode_mfma_supported(kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens);
+}
+
+int ie_hip_rope_cache_attention_supported(int kv_dtype, int n_heads, int n_kv_heads,
+                                          int head_dim, int chunk_tokens) {
+  return fused_supported(kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens) ? 1 : 0;
+}
+
+int ie_hip_rope_cache_attention(float* out, const float* q, const float* k, const float* v,
+                                void* k_pool, void* v_pool, const float* rope_table,
+                                int table_positions, int T, const int32_t* row_pos,
+                                const int32_t* row_seq, ie_kv_layout kv, int num_chunks,
+                                int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
+                                int head_dim, hipStream_t stream) {
+  clear_error();
+  if (int rc = check_layout(kv, "rope_cache_attention")) return rc;
+  if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0)
+    return fail(IE_HIP_EINVAL, "rope_cache_attention: bad head counts");
+  if (num_chunks <= 0 || T < 0) return fail(IE_HIP_EINVAL, "rope_cache_attention: bad chunk or row count");
+  if (table_positions <= 0) return fail(IE_HIP_EINVAL, "rope_cache_attention: empty RoPE table");
+  if (!fused_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens))
+    return fail(IE_HIP_EINVAL,
+                "rope_cache_attention: needs a 16-bit KV cache and the matrix-core decode shapes "
+                "(head_dim 64, kv_dim 128, n_heads <= 16, chunk a multiple of 64 up to 1024); "
+                "use ie_hip_rope_and_cache + ie_hip_attention");
+  if (T == 0) return IE_HIP_OK;
+  if (!out || !q || !k || !v || !k_pool || !v_pool || !rope_table || !row_pos || !row_seq ||
+      !workspace)
+    return fail(IE_HIP_EINVAL, "rope_cache_attention: null pointer");
+  if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(workspace) |
+       reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+       reinterpret_cast<uintptr_t>(rope_table)) & 15)
+    return fail(IE_HIP_EINVAL,
+                "rope_cache_attention: out, k, v, the table and the workspace must be 16-byte "
+                "aligned");
+  FusedAppend fa;
+  fa.k = k;
+  fa.v = v;
+  fa.k_pool = static_cast<uint16_t*>(k_pool);
+  fa.v_pool = static_cast<uint16_t*>(v_pool);
+  fa.table = rope_table;
+  fa.table_positions = table_positions;
+  return decode_mfma(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
+                     workspace, n_heads, n_kv_heads, stream, &fa);
+}
+
 }  // extern "C"

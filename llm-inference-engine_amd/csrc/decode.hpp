@@ -11,6 +11,18 @@ namespace iehip {
 inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 // The caller-owned decode workspace, carved into its parts.
+// The decode step's RoPE + append folded into the 16-bit attention launch:
+// the rows' new k/v (float32, unrotated), the pools to write them into, and
+// the host cos/sin table (ie_hip_rope_cache_attention).
+struct FusedAppend {
+  const float* k = nullptr;
+  const float* v = nullptr;
+  uint16_t* k_pool = nullptr;
+  uint16_t* v_pool = nullptr;
+  const float* table = nullptr;
+  int table_positions = 0;
+};
+
 struct Workspace {
   float* part_o = nullptr;     // [T][n_heads][num_chunks][head_dim] unnormalised partial outputs
   float* part_ml = nullptr;    // [T][n_heads][num_chunks][2] partial max and sum of exp
@@ -38,7 +50,8 @@ bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_d
 int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                 const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
-                hipStream_t stream);
+                hipStream_t stream,
+                const FusedAppend* fused = nullptr);
 
 int decode_valu(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                 const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,

@@ -117,14 +117,15 @@ __device__ __forceinline__ bool locate_chunk(int wg, int T, const int32_t* __res
 // kOneWave: one-wave workgroups (chunks of up to 255 tokens) -- the wave's
 // softmax is the chunk's, so the epilogue writes straight from the
 // accumulators and the workgroup needs no LDS beyond its V tiles.
-template <int KV, bool kOneWave>
-__global__ void __launch_bounds__(kOneWave ? 64 : 512) __attribute__((amdgpu_waves_per_eu(3)))
+template <int KV, bool kOneWave, bool kFused>
+__global__ void __launch_bounds__(kOneWave ? 64 : 512)
+__attribute__((amdgpu_waves_per_eu(kFused ? 2 : 3)))  // fused: the new row's registers too
 decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
                     float* __restrict__ part_ml, const float* __restrict__ q,
                     const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
                     const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
                     const int32_t* __restrict__ tables, int T, int max_pages, int num_pages,
-                    int n_heads, int group, int num_chunks, int chunk_tokens) {
+                    int n_heads, int group, int num_chunks, int chunk_tokens, FusedAppend fa) {
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
@@ -167,6 +168,85 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     q0b = qrow[1];
     q1a = qrow[8];
     q1b = qrow[9];
+  }
+
+  // Fused RoPE + append (kFused): every workgroup rotates its row's query in
+  // registers (lane (g, r) holds the rotation pairs (8g + j, 32 + 8g + j) of
+  // head r) with the table's cos/sin of position p; the wave holding position
+  // p -- the row's newest, appended now -- also rotates and rounds the new k,
+  // rounds v, writes both into their page slot and substitutes them for what
+  // it loads from there. Same arithmetic as ie_hip_rope_and_cache (explicit
+  // fmaf, no contraction; the KV type's own rounding), so pages and results
+  // are bit-identical to the two calls. Rows whose position lies outside the
+  // table are not appended and use their query unrotated, as there.
+  const bool app = kFused && p < fa.table_positions;
+  const int off = p - s0 - wt0;  // position p within this wave's range
+  const bool own = app && off >= 0 && off < tw;
+  E kn[4][8];                    // new K row, this lane's slices (dims 8g + 32 ks + e)
+  uint4 vn = make_uint4(0, 0, 0, 0);  // new V row, 16-byte piece r
+  if constexpr (kFused) {
+    if (app) {
+      const float* trow = fa.table + size_t(p) * 64 + 8 * g;
+      const float4 c0 = *reinterpret_cast<const float4*>(trow);
+      const float4 c1 = *reinterpret_cast<const float4*>(trow + 4);
+      const float4 n0 = *reinterpret_cast<const float4*>(trow + 32);
+      const float4 n1 = *reinterpret_cast<const float4*>(trow + 36);
+      const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const float sn[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+      auto rotate = [&](float4& a0, float4& a1, float4& b0, float4& b1) {
+        float x0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        float x1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float r0[8], r1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          r0[e] = __builtin_fmaf(x0[e], cs[e], -(x1[e] * sn[e]));  // x0*c - x1*s
+          r1[e] = __builtin_fmaf(x1[e], cs[e], x0[e] * sn[e]);     // x1*c + x0*s
+        }
+        a0 = make_float4(r0[0], r0[1], r0[2], r0[3]);
+        a1 = make_float4(r0[4], r0[5], r0[6], r0[7]);
+        b0 = make_float4(r1[0], r1[1], r1[2], r1[3]);
+        b1 = make_float4(r1[4], r1[5], r1[6], r1[7]);
+      };
+      rotate(q0a, q0b, q1a, q1b);
+      if (own) {
+        const float4* krow = reinterpret_cast<const float4*>(fa.k + size_t(t) * kKvd + 8 * g);
+#pragma unroll
+        for (int hk = 0; hk < 2; ++hk) {  // KV head hk: dims 64 hk + (8g .. 8g+7, 32 + ..)
+          float4 a0 = krow[16 * hk], a1 = krow[16 * hk + 1];
+          float4 b0 = krow[16 * hk + 8], b1 = krow[16 * hk + 9];
+          rotate(a0, a1, b0, b1);
+          const float ra[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+          const float rb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            kn[2 * hk][e] = __builtin_bit_cast(E, static_cast<uint16_t>(Kv<KV>::narrow(ra[e])));
+            kn[2 * hk + 1][e] = __builtin_bit_cast(E, static_cast<uint16_t>(Kv<KV>::narrow(rb[e])));
+          }
+        }
+        const float4* vrow = reinterpret_cast<const float4*>(fa.v + size_t(t) * kKvd + 8 * r);
+        const float4 v0 = vrow[0], v1 = vrow[1];
+        vn.x = Kv<KV>::narrow(v0.x) | (Kv<KV>::narrow(v0.y) << 16);
+        vn.y = Kv<KV>::narrow(v0.z) | (Kv<KV>::narrow(v0.w) << 16);
+        vn.z = Kv<KV>::narrow(v1.x) | (Kv<KV>::narrow(v1.y) << 16);
+        vn.w = Kv<KV>::narrow(v1.z) | (Kv<KV>::narrow(v1.w) << 16);
+        // The append itself: K slices from lanes (g, p % 16), V pieces from lanes
+        // (0, r); skipped, like ie_hip_rope_and_cache, when the page is outside
+        // the pool.
+        const int pidx = p / IE_HIP_PAGE_SIZE;
+        const int pid = pidx < max_pages ? tables[size_t(seq) * max_pages + pidx] : -1;
+        if (pid >= 0 && pid < num_pages) {
+          const size_t row = (size_t(pid) * IE_HIP_PAGE_SIZE + (p & 15)) * kKvd;
+          if (r == (p & 15)) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+              *reinterpret_cast<op*>(fa.k_pool + row + 8 * g + 32 * ks) =
+                  op{kn[ks][0], kn[ks][1], kn[ks][2], kn[ks][3],
+                     kn[ks][4], kn[ks][5], kn[ks][6], kn[ks][7]};
+          }
+          if (g == 0) *reinterpret_cast<uint4*>(fa.v_pool + row + 8 * r) = vn;
+        }
+      }
+    }
   }
 
   // Loads of page pair j (pages 2j, 2j+1 of the wave): K into the MFMA
@@ -248,6 +328,18 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   for (int j = 0; j < np; ++j) {
     // Outstanding: K and V of pair j (8 + 8 loads, in that order).
     wait_vmcnt<8>();
+    if constexpr (kFused) {
+      if (own && j == (off >> 5) && r == (p & 15)) {  // position p's K row: the new one
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          if (h == ((off >> 4) & 1)) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+              ka[h][ks] = op{kn[ks][0], kn[ks][1], kn[ks][2], kn[ks][3],
+                             kn[ks][4], kn[ks][5], kn[ks][6], kn[ks][7]};
+          }
+      }
+    }
     f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = sa;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -314,6 +406,15 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if constexpr (kFused) {
+      // Position p's V row in the tile: the new one (ahead of the transposed
+      // reads below in the wave's LDS queue).
+      if (own && j == (off >> 5) && g == 0) {
+        const int tok = off & 31;
+        *reinterpret_cast<uint4*>(warea + (j & 1) * kPair + tok * 256 +
+                                  16 * (r ^ (2 * (tok & 7)))) = vn;
+      }
+    }
     unsigned long long keep_lo = ~0ull, keep_hi = ~0ull;
     if (!full) {  // 0 * (stale inf or NaN) is not 0: zero masked V elements
       keep_lo = keep_hi = 0;
@@ -609,7 +710,7 @@ static int decode_mfma_waves(int chunk_tokens, int64_t slots) {
 int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                 const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
-                hipStream_t stream) {
+                hipStream_t stream, const FusedAppend* fused) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
   const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
   const int waves = decode_mfma_waves(chunk_tokens, slots);
@@ -624,31 +725,38 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
   const uint16_t* kp = static_cast<const uint16_t*>(k_pool);
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
   // 8 waves (1024-token chunks) take 128 KB of LDS: above the 64 KB default cap
-  // for dynamic LDS, within gfx950's 160 KB per workgroup. Raise it once.
-  static const hipError_t attr_f16 = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_F16, false>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
-  static const hipError_t attr_bf16 = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(decode_partial_mfma<IE_KV_BF16, false>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
-  if (int rc = check_hip(kv.kv_dtype == IE_KV_F16 ? attr_f16 : attr_bf16,
-                         "hipFuncSetAttribute(attention_partial_mfma)"))
-    return rc;
-#define IE_DECODE_LAUNCH(KVT, ONE)                                                              \
-  hipLaunchKernelGGL((decode_partial_mfma<KVT, ONE>), grid, block, lds, stream, out, ws.part_o, \
-                     ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, T, kv.max_pages,      \
-                     kv.num_pages, n_heads, group, num_chunks, chunk_tokens)
-  if (kv.kv_dtype == IE_KV_F16) {
-    if (waves == 1)
-      IE_DECODE_LAUNCH(IE_KV_F16, true);
-    else
-      IE_DECODE_LAUNCH(IE_KV_F16, false);
-  } else {
-    if (waves == 1)
-      IE_DECODE_LAUNCH(IE_KV_BF16, true);
-    else
-      IE_DECODE_LAUNCH(IE_KV_BF16, false);
+  // for dynamic LDS, within gfx950's 160 KB per workgroup. Raised once per kernel.
+  const FusedAppend fa = fused ? *fused : FusedAppend{};
+#define IE_DECODE_LAUNCH(KVT, ONE, FUSED)                                                         \
+  do {                                                                                            \
+    if (!(ONE)) {                                                                                 \
+      static const hipError_t attr = hipFuncSetAttribute(                                         \
+          reinterpret_cast<const void*>(decode_partial_mfma<KVT, ONE, FUSED>),                    \
+          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);                                   \
+      if (int rc = check_hip(attr, "hipFuncSetAttribute(attention_partial_mfma)")) return rc;     \
+    }                                                                                             \
+    hipLaunchKernelGGL((decode_partial_mfma<KVT, ONE, FUSED>), grid, block, lds, stream, out,     \
+                       ws.part_o, ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, T,          \
+                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens, fa); \
+  } while (0)
+#define IE_DECODE_LAUNCH_KV(KVT)                 \
+  if (fused) {                                   \
+    if (waves == 1)                              \
+      IE_DECODE_LAUNCH(KVT, true, true);         \
+    else                                         \
+      IE_DECODE_LAUNCH(KVT, false, true);        \
+  } else {                                       \
+    if (waves == 1)                              \
+      IE_DECODE_LAUNCH(KVT, true, false);        \
+    else                                         \
+      IE_DECODE_LAUNCH(KVT, false, false);       \
   }
+  if (kv.kv_dtype == IE_KV_F16) {
+    IE_DECODE_LAUNCH_KV(IE_KV_F16)
+  } else {
+    IE_DECODE_LAUNCH_KV(IE_KV_BF16)
+  }
+#undef IE_DECODE_LAUNCH_KV
 #undef IE_DECODE_LAUNCH
   if (int rc = check_launch("attention_mfma")) return rc;
   return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
