@@ -1,6 +1,8 @@
-// Flash-decoding attention over pages on the matrix cores (gfx950), for f16
-// and bf16 KV caches whose rows hold 128 elements (2 KV heads x 64) and at
-// most 16 query heads -- Qwen2.5-0.5B: 14 query heads, 2 KV heads.
+// Flash-decoding attention over pages on the matrix cores (gfx950), for KV
+// caches whose rows hold 128 elements (2 KV heads x 64) and at most 16 query
+// heads -- Qwen2.5-0.5B: 14 query heads, 2 KV heads. 16-bit caches:
+// decode_partial_mfma, described here (with kFused, the decode step's RoPE +
+// append rides along); f32 caches: decode_partial_mfma_f32, further down.
 //
 // Reference semantics: each row's causal GQA attention, src/ops.cpp:70-108;
 // split-K chunks merged by log-sum-exp as in src/cuda/kernels.cu:309-507.

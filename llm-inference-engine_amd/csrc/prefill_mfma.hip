@@ -1,5 +1,7 @@
-// Chunked-prefill attention into pages on the matrix cores (gfx950), for f16
-// and bf16 KV caches with head_dim 64.
+// Chunked-prefill attention into pages on the matrix cores (gfx950), for KV
+// caches of every type with head_dim 64: 16-bit caches on the 16-bit
+// instructions (prefill_mfma_kernel), f32 caches on the f32 ones
+// (prefill_mfma_f32_kernel, further down).
 //
 // Reference semantics: each row's causal GQA attention over positions
 // 0..row_pos[t] of its sequence (src/ops.cpp:70-108); the reference's GPU
@@ -24,17 +26,20 @@
 //   One workgroup per (pair of 16-row blocks, KV head); one wave per query head
 //   of the KV head (the 7 heads of a Qwen2.5 group share every K/V tile through
 //   LDS). Two heads per wave (each K/V operand feeding both) was measured
-//   slower: half the waves leave the dependency and barrier stalls exposed. The pair is block b and block n-1-b: the causal triangle gives block b
-//   b+1 key tiles of work, so every pair carries about the same total and the
+//   slower: half the waves leave the dependency and barrier stalls exposed.
+//   The pair is block b and block n-1-b: the causal triangle gives block b b+1
+//   key tiles of work, so every pair carries about the same total and the
 //   ceil(n/2) x n_kv_heads workgroups finish together (the heavier block goes
-//   first).
-//   K/V tiles of 64 keys (4 pages) go through a ring of 4 LDS buffers (4 x 16 KB):
-//   while the waves compute on one, the next three tiles' 16 KB each are in
-//   flight by DMA (global_load_lds_dwordx4, 16 x 1 KB spread evenly over the waves),
-//   page ids read a tile ahead. K rows are stored with their 16-byte pieces
-//   swizzled (piece ^ (row/2 % 8)) so the A-operand reads (16 rows, one piece
-//   each) hit distinct banks; V rows with piece ^ 2*(row/2 % 4) so the
-//   transposed reads (ds_read_b64_tr_b16: 8 rows x 32 bytes per half-wave) do.
+//   first). When that grid leaves compute units with at most one workgroup,
+//   two teams of waves split each block's key tiles (even and odd) and merge
+//   their (m, l, O) through LDS at the end.
+//   K/V tiles of 64 keys (4 pages, 16 KB) go through an LDS ring by DMA
+//   (global_load_lds_dwordx4, 16 x 1 KB per tile spread over 4 waves of a team):
+//   4 tiles with one team, 3 steps of 2 tiles with two; page ids are read a
+//   step ahead. K rows are stored with their 16-byte pieces swizzled
+//   (piece ^ (row/2 % 8)) so the A-operand reads (16 rows, one piece each) hit
+//   distinct banks; V rows with piece ^ 2*(row/2 % 4) so the transposed reads
+//   (ds_read_b64_tr_b16: 8 rows x 32 bytes per half-wave) do.
 //   Keys past the block's last position and pages outside the pool are masked
 //   (-inf scores, and their V rows zeroed in LDS before use, so stale or
 //   non-finite memory cannot reach the output through 0 * x).
