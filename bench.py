@@ -207,7 +207,7 @@ def bench_decode(args, torch, ie, O):
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles("decode")},
+                     "traffic": traffic_from_profiles("decode", kv, "f16", args)},
         "algorithmic_bytes_per_step": nbytes,
         "warm_mall": {"ms_per_step": round(ms_warm, 5),
                       "gbs": round(nbytes / (ms_warm * 1e-3) / 1e9, 2),
@@ -267,7 +267,7 @@ def bench_append(args, torch, ie, O):
                                "65,536-page pool", "kv_dtype": kv, "seed": args.seed},
         "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 5),
-                     "traffic": traffic_from_profiles("append")},
+                     "traffic": traffic_from_profiles("append", kv, "f16", args)},
         "sweep": sweep,
     }
 
@@ -333,7 +333,8 @@ def bench_long(args, torch, ie, O):
         "tok_per_s": round(1 / (ms * 1e-3), 1), "us_per_layer": round(ms * 1e3 / layers, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles("long")},
+                     "traffic": traffic_from_profiles("long" if fused else "long_unfused",
+                                                      kv, "bf16", args)},
         "algorithmic_bytes_per_step": nbytes,
     }
 
@@ -428,14 +429,16 @@ def bench_mixed(args, torch, ie, O):
     }
 
 
-def traffic_from_profiles(kernel: str):
+def traffic_from_profiles(key: str, kv: str, default_kv: str, args):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE runs, as committed
-    under profiles/ (null when that measurement has not been made)."""
+    under profiles/: `key` for the workload's default KV type, `key_<kv>` for another.
+    Null when that measurement has not been made, or when the chunk size is overridden
+    (the counters were read at the library's own choice)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
-    if not os.path.exists(path):
+    if args.chunk_tokens or not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get(kernel)
+        return json.load(f).get(key if kv == default_kv else f"{key}_{kv}")
 
 
 def copy_probe(torch, n_bytes=2 << 30):
