@@ -35,9 +35,11 @@
 //   their (m, l, O) through LDS at the end.
 //   K/V tiles of 64 keys (4 pages, 16 KB) go through an LDS ring by DMA
 //   (global_load_lds_dwordx4, 16 x 1 KB per tile spread over 4 waves of a team):
-//   4 tiles with one team, 3 steps of 2 tiles with two; page ids are read a
-//   step ahead. K rows are stored with their 16-byte pieces swizzled
-//   (piece ^ (row/2 % 8)) so the A-operand reads (16 rows, one piece each) hit
+//   4 tiles with one team, 3 steps of 2 tiles with two. The page ids of up to
+//   512 tiles are staged in LDS at a block's start (scalar loads of the table
+//   inside the loop would share lgkmcnt with the K reads and put the table's
+//   round trip on every step). K rows are stored with their 16-byte pieces
+//   swizzled (piece ^ (row/2 % 8)) so the A-operand reads (16 rows, one piece each) hit
 //   distinct banks; V rows with piece ^ 2*(row/2 % 4) so the transposed reads
 //   (ds_read_b64_tr_b16: 8 rows x 32 bytes per half-wave) do.
 //   Keys past the block's last position and pages outside the pool are masked
@@ -61,6 +63,7 @@ constexpr int kHeadsPerWave = 1;           // query heads per wave (2 measured s
 static_assert(kHeadsPerWave == 1, "the team exchange hands over one head per wave");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;           // log2 headroom of the lazily raised softmax max
+constexpr int kSegTiles = 512;             // key tiles (32,768 keys) with page ids in LDS at once
 
 // kWaves = group / kHeadsPerWave waves per team (rounded up), wave w of a team
 // taking query heads kHeadsPerWave * w .. of the KV head. kTeams teams of
@@ -77,6 +80,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   using op = typename M::op;
   using E = typename M::elem;
   constexpr int kRingSteps = kTeams == 1 ? 4 : 3;  // steps of kTeams tiles in LDS
+  constexpr int kRingBytes = kRingSteps * kTeams * kBufBytes;
   op ones;  // all-ones A operand: row sums of P^T on the matrix cores
 #pragma unroll
   for (int i = 0; i < 8; ++i) ones[i] = static_cast<E>(1.0f);
@@ -97,12 +101,22 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   const int seq = __builtin_amdgcn_readfirstlane(row_seq[0]);
   const int32_t* tab = tables + size_t(seq) * max_pages;
 
-  // Page id of the tile's page j (uniform); -1 past the table row.
-  auto page_id = [&](const int tile, const int j) -> int {
-    const int pi = tile * (kKeys / IE_HIP_PAGE_SIZE) + j;
-    return pi < max_pages ? tab[pi] : -1;
+  // The page ids of a segment of key tiles, staged in LDS after the ring by all
+  // threads at the segment's start: ids[4 (tile - seg0) + j] is page j of the
+  // tile, or -1 for a page past the table row or outside the pool (loaded as
+  // page 0 and masked). A step then reads its tiles' ids from LDS instead of
+  // the table: no memory round trip inside the tile loop.
+  int* const ids = reinterpret_cast<int*>(smem + kRingBytes);
+  int seg0 = 0;  // first tile of the segment in progress
+  auto tile_ids = [&](const int tile) {
+    return *reinterpret_cast<const int4*>(ids + 4 * (tile - seg0));
   };
-  auto valid = [&](const int id) { return id >= 0 && id < num_pages; };
+  // Bit j set: page j of the tile is inside the pool (uniform).
+  auto tile_ok = [&](const int tile) -> int {
+    const int4 v = tile_ids(tile);
+    return __builtin_amdgcn_readfirstlane(int(v.x >= 0) | (int(v.y >= 0) << 1) |
+                                          (int(v.z >= 0) << 2) | (int(v.w >= 0) << 3));
+  };
   // Buffer of the tile a team takes at step s.
   auto buffer = [&](const int ring_step, const int tm) { return ring_step * kTeams + tm; };
 
@@ -125,8 +139,13 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   const char* kbase_g = reinterpret_cast<const char*>(k_pool) + kvh * 128;
   const char* vbase_g = reinterpret_cast<const char*>(v_pool) + kvh * 128;
   const size_t page_bytes = size_t(IE_HIP_PAGE_SIZE) * row_bytes;
-  auto issue = [&](const int buf, const int* id) {
+  auto issue = [&](const int buf, const int tile) {
     if (wave >= kDmaWaves) return;
+    const int4 v = tile_ids(tile);
+    const int id[4] = {max(__builtin_amdgcn_readfirstlane(v.x), 0),
+                       max(__builtin_amdgcn_readfirstlane(v.y), 0),
+                       max(__builtin_amdgcn_readfirstlane(v.z), 0),
+                       max(__builtin_amdgcn_readfirstlane(v.w), 0)};
     // Quarter qt of the loads: qt = 0, 1 the K rows 0-31, 32-63; qt = 2, 3 the V rows.
 #pragma unroll
     for (int k = 0; k < 4 / kDmaWaves; ++k) {
@@ -135,8 +154,8 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       const int half = qt & 1;  // rows 32 half .. 32 half + 31: pages 2 half, 2 half + 1
       const int ida = half ? id[2] : id[0], idb = half ? id[3] : id[1];
       const char* base = is_v ? vbase_g : kbase_g;
-      const char* pa = base + size_t(valid(ida) ? ida : 0) * page_bytes;
-      const char* pb = base + size_t(valid(idb) ? idb : 0) * page_bytes;
+      const char* pa = base + size_t(ida) * page_bytes;
+      const char* pb = base + size_t(idb) * page_bytes;
       const unsigned dst = smem_lds + buf * kBufBytes + (is_v ? kTileBytes : 0) + half * 4096;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {  // u = 4 half + j: page u / 2 of the tile
@@ -161,7 +180,6 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     const int max_pos = pos0 + t_last;  // last position any row of the block sees
     const int min_pos = pos0 + t0;      // first row's position
     const int n_tiles = max_pos / kKeys + 1;
-    const int n_steps = (n_tiles + kTeams - 1) / kTeams;
 
     // Queries of row t0 + r for the wave's heads, times log2(e)/8, split hi + lo:
     // the B operands of S^T (dims 32 ks + 8g .. +8).
@@ -210,217 +228,192 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       for (int mt = 0; mt < 4; ++mt) o[hh][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // Ring of kRingSteps steps of kTeams tile buffers: steps 0 .. kRingSteps-2
-    // are issued up front; at step s, step s + kRingSteps - 1 goes into the
-    // buffers step s - 1 used. Every wave reads the page ids of every tile of a
-    // step (one step ahead of its DMA): `okq` queues 4 "page inside the pool"
-    // bits per tile in flight (step s's tiles in the lowest 4 kTeams bits), so
-    // that the zeroing decision below is the same in every wave. A step past the
-    // last tile still loads (in-pool pages, never read), keeping every step's
-    // load count the same for the counted waits.
-    constexpr int kStepBits = 4 * kTeams;
-    int nx[kTeams][4];
-    auto read_ids = [&](const int step) {
-#pragma unroll
-      for (int tm = 0; tm < kTeams; ++tm)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) nx[tm][j] = page_id(kTeams * step + tm, j);
-    };
-    // This team's tile ids of the step held in nx (selected, not indexed by the
-    // run-time team, which would put nx in scratch memory).
-    auto mine = [&](int (&id)[4]) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) id[j] = (kTeams == 1 || team == 0) ? nx[0][j] : nx[kTeams - 1][j];
-    };
-    auto ok_bits = [&]() {
-      int b = 0;
-#pragma unroll
-      for (int tm = 0; tm < kTeams; ++tm)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b |= int(valid(nx[tm][j])) << (4 * tm + j);
-      return b;
-    };
-    read_ids(0);
-    int okq = 0;
-    for (int pre = 0; pre < kRingSteps - 1 && pre < n_steps; ++pre) {
-      okq |= ok_bits() << (kStepBits * pre);
-      int id[4];
-      mine(id);
-      issue(buffer(pre, team), id);
-      read_ids(pre + 1);
-    }
-    wait_steps(min(kRingSteps - 2, n_steps - 1));  // step 0 has landed
-    __syncthreads();
+    // The block's key tiles in segments of kSegTiles, each with its page ids
+    // staged in LDS. Within a segment, a ring of kRingSteps steps of kTeams tile
+    // buffers: steps 0 .. kRingSteps-2 are issued up front; at step s, step
+    // s + kRingSteps - 1 goes into the buffers step s - 1 used. A step past the
+    // last tile still loads (page 0 or in-pool pages, never read), keeping every
+    // step's load count the same for the counted waits. Segments hold an even
+    // number of tiles, so a step never straddles two.
+    for (seg0 = 0; seg0 < n_tiles; seg0 += kSegTiles) {
+      const int n_steps = (min(kSegTiles, n_tiles - seg0) + kTeams - 1) / kTeams;
+      // The ring is idle here and every wave is past its last read of the previous
+      // segment's ids (the last step, or the team exchange, ended in a barrier).
+      for (int i = tid; i < 4 * kTeams * n_steps; i += 64 * kWaves * kTeams) {
+        const int pi = 4 * seg0 + i;
+        const int id = pi < max_pages ? tab[pi] : -1;
+        ids[i] = id >= 0 && id < num_pages ? id : -1;
+      }
+      __syncthreads();
+      for (int pre = 0; pre < kRingSteps - 1 && pre < n_steps; ++pre)
+        issue(buffer(pre, team), seg0 + kTeams * pre + team);
+      wait_steps(min(kRingSteps - 2, n_steps - 1));  // step 0 has landed
+      __syncthreads();
 
-    int rs = 0;                    // ring slot of step s
-    int is = kRingSteps - 1;       // ring slot of step s + kRingSteps - 1
-    for (int st = 0; st < n_steps; ++st) {
-      const int oks = okq & ((1 << kStepBits) - 1);
-      okq >>= kStepBits;
-      const int ahead = st + kRingSteps - 1;
-      if (ahead < n_steps) {  // its buffers held step s - 1: free since the last barrier
-        okq |= ok_bits() << (kStepBits * (kRingSteps - 2));
-        int id[4];
-        mine(id);
-        issue(buffer(is, team), id);
-        read_ids(ahead + 1);
-      }
-      is = is + 1 == kRingSteps ? 0 : is + 1;
-      const int kb = kTeams * st + team;  // this team's tile
-      const int okb = (oks >> (4 * team)) & 15;
-      const int buf = buffer(rs, team);
-      rs = rs + 1 == kRingSteps ? 0 : rs + 1;
-      const int kbase = kb * kKeys;
-      const unsigned char* kt = smem + buf * kBufBytes;
-      unsigned char* vt = smem + buf * kBufBytes + kTileBytes;
-      // Keys past max_pos (the last tile) or in pages outside the pool: zero
-      // their V rows before the team reads the tile. The decision covers every
-      // tile of the step, so every wave takes the same branch and barrier.
-      bool zero_step = false;
+      int rs = 0;               // ring slot of step s
+      int is = kRingSteps - 1;  // ring slot of step s + kRingSteps - 1
+      for (int st = 0; st < n_steps; ++st) {
+        const int ahead = st + kRingSteps - 1;
+        if (ahead < n_steps)  // its buffers held step s - 1: free since the last barrier
+          issue(buffer(is, team), seg0 + kTeams * ahead + team);
+        is = is + 1 == kRingSteps ? 0 : is + 1;
+        const int kb = seg0 + kTeams * st + team;  // this team's tile
+        const int buf = buffer(rs, team);
+        rs = rs + 1 == kRingSteps ? 0 : rs + 1;
+        const int kbase = kb * kKeys;
+        const unsigned char* kt = smem + buf * kBufBytes;
+        unsigned char* vt = smem + buf * kBufBytes + kTileBytes;
+        // Keys past max_pos (the last tile) or in pages outside the pool: zero
+        // their V rows before the team reads the tile. The decision covers every
+        // tile of the step, so every wave takes the same branch and barrier.
+        bool zero_step = false;
 #pragma unroll
-      for (int tm = 0; tm < kTeams; ++tm) {
-        const int tile = kTeams * st + tm;
-        zero_step |= tile < n_tiles &&
-                     (tile * kKeys + kKeys - 1 > max_pos || ((oks >> (4 * tm)) & 15) != 15);
-      }
-      if (zero_step) {
-        if (kb < n_tiles) {
-          for (int i = tid - 64 * kWaves * team; i < kKeys * 8; i += 64 * kWaves) {
-            const int key = i >> 3;
-            if (kbase + key > max_pos || !((okb >> (key >> 4)) & 1))
-              *reinterpret_cast<uint4*>(vt + key * 128 + (i & 7) * 16) = make_uint4(0, 0, 0, 0);
-          }
+        for (int tm = 0; tm < kTeams; ++tm) {
+          const int tile = seg0 + kTeams * st + tm;
+          if (tile < n_tiles)
+            zero_step |= tile * kKeys + kKeys - 1 > max_pos || tile_ok(tile) != 15;
         }
-        __syncthreads();
-      }
-
-      if (kb < n_tiles) {  // uniform per team (the odd last step of team 1 skips)
-        // S^T for the tile's 4 key groups of 16: A = K rows 16 kt4 + r, dims 32 ks + 8g.
-        op ka[4][2];
-#pragma unroll
-        for (int kt4 = 0; kt4 < 4; ++kt4) {
-          const int row = 16 * kt4 + r;
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
-            ka[kt4][ks] = *reinterpret_cast<const op*>(kt + row * 128 +
-                                                       16 * ((4 * ks + g) ^ ((row >> 1) & 7)));
-        }
-        // The accumulators start at -mref (the row's reference max, 0 before any
-        // visible key), so the products come out as s - mref directly.
-        float mref[kHeadsPerWave];
-#pragma unroll
-        for (int hh = 0; hh < kHeadsPerWave; ++hh) mref[hh] = m[hh] == -INFINITY ? 0.0f : m[hh];
-        f32x4 s[kHeadsPerWave][4];
-#pragma unroll
-        for (int kt4 = 0; kt4 < 4; ++kt4)
-#pragma unroll
-          for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-            f32x4 acc = {-mref[hh], -mref[hh], -mref[hh], -mref[hh]};
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              acc = M::mma(ka[kt4][ks], qhi[hh][ks], acc);
-              acc = M::mma(ka[kt4][ks], qlo[hh][ks], acc);
+        const int okb = kb < n_tiles ? tile_ok(kb) : 0;
+        if (zero_step) {
+          if (kb < n_tiles) {
+            for (int i = tid - 64 * kWaves * team; i < kKeys * 8; i += 64 * kWaves) {
+              const int key = i >> 3;
+              if (kbase + key > max_pos || !((okb >> (key >> 4)) & 1))
+                *reinterpret_cast<uint4*>(vt + key * 128 + (i & 7) * 16) = make_uint4(0, 0, 0, 0);
             }
-            s[hh][kt4] = acc;
           }
-        // Causal mask (and masked pages) where the tile is not entirely visible.
-        if (kbase + kKeys - 1 > min_pos || okb != 15) {
+          __syncthreads();
+        }
+
+        if (kb < n_tiles) {  // uniform per team (the odd last step of team 1 skips)
+          // S^T for the tile's 4 key groups of 16: A = K rows 16 kt4 + r, dims 32 ks + 8g.
+          op ka[4][2];
+#pragma unroll
+          for (int kt4 = 0; kt4 < 4; ++kt4) {
+            const int row = 16 * kt4 + r;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+              ka[kt4][ks] = *reinterpret_cast<const op*>(kt + row * 128 +
+                                                         16 * ((4 * ks + g) ^ ((row >> 1) & 7)));
+          }
+          // The accumulators start at -mref (the row's reference max, 0 before any
+          // visible key), so the products come out as s - mref directly.
+          float mref[kHeadsPerWave];
+#pragma unroll
+          for (int hh = 0; hh < kHeadsPerWave; ++hh) mref[hh] = m[hh] == -INFINITY ? 0.0f : m[hh];
+          f32x4 s[kHeadsPerWave][4];
 #pragma unroll
           for (int kt4 = 0; kt4 < 4; ++kt4)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int kp = kbase + 16 * kt4 + 4 * g + e;
-              const bool vis = kp <= rp && ((okb >> kt4) & 1);
-#pragma unroll
-              for (int hh = 0; hh < kHeadsPerWave; ++hh)
-                s[hh][kt4][e] = vis ? s[hh][kt4][e] : -INFINITY;
-            }
-        }
-        // Online softmax per head on s - mref; P^T operands per 32-key group kg:
-        // slots 0-3 = keys 32kg + 4g + e (group 2kg), slots 4-7 = keys 32kg + 16 +
-        // 4g + e. The reference max m is raised lazily: weights are 2^(s - m) with
-        // m the row's max when it was last raised, and O and l are rescaled only
-        // when some row of the wave sees its max grow past m + kLazyMax (so weights
-        // stay below 2^kLazyMax, which the 16-bit hi + lo split carries at full
-        // precision). The row sums l come from the matrix cores (below).
-        op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
-#pragma unroll
-        for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-          float mx = -INFINITY;
-#pragma unroll
-          for (int kt4 = 0; kt4 < 4; ++kt4)
-            mx = fmaxf(mx, fmaxf(fmaxf(s[hh][kt4][0], s[hh][kt4][1]),
-                                 fmaxf(s[hh][kt4][2], s[hh][kt4][3])));
-          mx = group_max4(mx);  // the tile's row max, relative to mref
-          // m = -inf (nothing visible yet) always counts as growth when mx is finite.
-          const bool grow = m[hh] == -INFINITY ? mx != -INFINITY : mx > kLazyMax;
-          if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-            const float m_new = fmaxf(m[hh], mref[hh] + mx);
-            const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m[hh] - m_new);  // m = -inf: 0
-            lacc[hh] *= corr;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
-            m[hh] = m_new;
-            // Re-reference this tile's scores to the new max.
-            const float shift = (m_new == -INFINITY ? 0.0f : m_new) - mref[hh];
-#pragma unroll
-            for (int kt4 = 0; kt4 < 4; ++kt4) s[hh][kt4] -= shift;
-          }
-#pragma unroll
-          for (int kg = 0; kg < 2; ++kg)
-#pragma unroll
-            for (int e = 0; e < 4; e += 2) {
-              const float pa0 = exp2_weight(s[hh][2 * kg][e]);
-              const float pa1 = exp2_weight(s[hh][2 * kg][e + 1]);
-              const float pb0 = exp2_weight(s[hh][2 * kg + 1][e]);
-              const float pb1 = exp2_weight(s[hh][2 * kg + 1][e + 1]);
-              E h0, h1, l0, l1;
-              split16x2(pa0, pa1, h0, h1, l0, l1);
-              phi[hh][kg][e] = h0;
-              phi[hh][kg][e + 1] = h1;
-              plo[hh][kg][e] = l0;
-              plo[hh][kg][e + 1] = l1;
-              split16x2(pb0, pb1, h0, h1, l0, l1);
-              phi[hh][kg][4 + e] = h0;
-              phi[hh][kg][5 + e] = h1;
-              plo[hh][kg][4 + e] = l0;
-              plo[hh][kg][5 + e] = l1;
-            }
-          // Row sums: an all-ones A operand against P^T puts sum_k P[r][k] of the
-          // tile's 32-key group in every entry of lane r's accumulator.
-#pragma unroll
-          for (int kg = 0; kg < 2; ++kg) {
-            lacc[hh] = M::mma(ones, phi[hh][kg], lacc[hh]);
-            lacc[hh] = M::mma(ones, plo[hh][kg], lacc[hh]);
-          }
-        }
-        // O^T += V^T P^T. Lane L reads tile row 32kg + 4g + L/4 (and +16), dims
-        // 16 mt + 4 (L%4) .. +3: after the transpose lane r holds dim 16 mt + r of
-        // keys 32kg + 4g + e and 32kg + 16 + 4g + e -- P^T's slots.
-        const int rbyte = (r & 1) * 8;
-#pragma unroll
-        for (int kg = 0; kg < 2; ++kg) {
-          const int vrow = 32 * kg + 4 * g + (r >> 2);
-          const int sw = 2 * ((vrow >> 1) & 3);  // same for vrow + 16
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) {
-            const int slot = (2 * mt + ((r >> 1) & 1)) ^ sw;
-            const s16x4 lo4 = lds_read_tr16(vt + vrow * 128 + slot * 16 + rbyte);
-            const s16x4 hi4 = lds_read_tr16(vt + (vrow + 16) * 128 + slot * 16 + rbyte);
-            const op a = join_tr<op>(lo4, hi4);
 #pragma unroll
             for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-              o[hh][mt] = M::mma(a, phi[hh][kg], o[hh][mt]);
-              o[hh][mt] = M::mma(a, plo[hh][kg], o[hh][mt]);
+              f32x4 acc = {-mref[hh], -mref[hh], -mref[hh], -mref[hh]};
+#pragma unroll
+              for (int ks = 0; ks < 2; ++ks) {
+                acc = M::mma(ka[kt4][ks], qhi[hh][ks], acc);
+                acc = M::mma(ka[kt4][ks], qlo[hh][ks], acc);
+              }
+              s[hh][kt4] = acc;
+            }
+          // Causal mask (and masked pages) where the tile is not entirely visible.
+          if (kbase + kKeys - 1 > min_pos || okb != 15) {
+#pragma unroll
+            for (int kt4 = 0; kt4 < 4; ++kt4)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int kp = kbase + 16 * kt4 + 4 * g + e;
+                const bool vis = kp <= rp && ((okb >> kt4) & 1);
+#pragma unroll
+                for (int hh = 0; hh < kHeadsPerWave; ++hh)
+                  s[hh][kt4][e] = vis ? s[hh][kt4][e] : -INFINITY;
+              }
+          }
+          // Online softmax per head on s - mref; P^T operands per 32-key group kg:
+          // slots 0-3 = keys 32kg + 4g + e (group 2kg), slots 4-7 = keys 32kg + 16 +
+          // 4g + e. The reference max m is raised lazily: weights are 2^(s - m) with
+          // m the row's max when it was last raised, and O and l are rescaled only
+          // when some row of the wave sees its max grow past m + kLazyMax (so weights
+          // stay below 2^kLazyMax, which the 16-bit hi + lo split carries at full
+          // precision). The row sums l come from the matrix cores (below).
+          op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
+#pragma unroll
+          for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt4 = 0; kt4 < 4; ++kt4)
+              mx = fmaxf(mx, fmaxf(fmaxf(s[hh][kt4][0], s[hh][kt4][1]),
+                                   fmaxf(s[hh][kt4][2], s[hh][kt4][3])));
+            mx = group_max4(mx);  // the tile's row max, relative to mref
+            // m = -inf (nothing visible yet) always counts as growth when mx is finite.
+            const bool grow = m[hh] == -INFINITY ? mx != -INFINITY : mx > kLazyMax;
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+              const float m_new = fmaxf(m[hh], mref[hh] + mx);
+              // m = -inf (nothing seen yet): the old terms are all zero
+              const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m[hh] - m_new);
+              lacc[hh] *= corr;
+#pragma unroll
+              for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
+              m[hh] = m_new;
+              // Re-reference this tile's scores to the new max.
+              const float shift = (m_new == -INFINITY ? 0.0f : m_new) - mref[hh];
+#pragma unroll
+              for (int kt4 = 0; kt4 < 4; ++kt4) s[hh][kt4] -= shift;
+            }
+#pragma unroll
+            for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+              for (int e = 0; e < 4; e += 2) {
+                const float pa0 = exp2_weight(s[hh][2 * kg][e]);
+                const float pa1 = exp2_weight(s[hh][2 * kg][e + 1]);
+                const float pb0 = exp2_weight(s[hh][2 * kg + 1][e]);
+                const float pb1 = exp2_weight(s[hh][2 * kg + 1][e + 1]);
+                E h0, h1, l0, l1;
+                split16x2(pa0, pa1, h0, h1, l0, l1);
+                phi[hh][kg][e] = h0;
+                phi[hh][kg][e + 1] = h1;
+                plo[hh][kg][e] = l0;
+                plo[hh][kg][e + 1] = l1;
+                split16x2(pb0, pb1, h0, h1, l0, l1);
+                phi[hh][kg][4 + e] = h0;
+                phi[hh][kg][5 + e] = h1;
+                plo[hh][kg][4 + e] = l0;
+                plo[hh][kg][5 + e] = l1;
+              }
+            // Row sums: an all-ones A operand against P^T puts sum_k P[r][k] of the
+            // tile's 32-key group in every entry of lane r's accumulator.
+#pragma unroll
+            for (int kg = 0; kg < 2; ++kg) {
+              lacc[hh] = M::mma(ones, phi[hh][kg], lacc[hh]);
+              lacc[hh] = M::mma(ones, plo[hh][kg], lacc[hh]);
+            }
+          }
+          // O^T += V^T P^T. Lane L reads tile row 32kg + 4g + L/4 (and +16), dims
+          // 16 mt + 4 (L%4) .. +3: after the transpose lane r holds dim 16 mt + r of
+          // keys 32kg + 4g + e and 32kg + 16 + 4g + e -- P^T's slots.
+          const int rbyte = (r & 1) * 8;
+#pragma unroll
+          for (int kg = 0; kg < 2; ++kg) {
+            const int vrow = 32 * kg + 4 * g + (r >> 2);
+            const int sw = 2 * ((vrow >> 1) & 3);  // same for vrow + 16
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+              const int slot = (2 * mt + ((r >> 1) & 1)) ^ sw;
+              const s16x4 lo4 = lds_read_tr16(vt + vrow * 128 + slot * 16 + rbyte);
+              const s16x4 hi4 = lds_read_tr16(vt + (vrow + 16) * 128 + slot * 16 + rbyte);
+              const op a = join_tr<op>(lo4, hi4);
+#pragma unroll
+              for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+                o[hh][mt] = M::mma(a, phi[hh][kg], o[hh][mt]);
+                o[hh][mt] = M::mma(a, plo[hh][kg], o[hh][mt]);
+              }
             }
           }
         }
+        // This wave's loads of step s + 1 have landed (later steps may still be in
+        // flight); after the barrier every wave's have, and every wave is done
+        // with step s's buffers.
+        wait_steps(max(0, min(kRingSteps - 2, n_steps - st - 2)));
+        __syncthreads();
       }
-      // This wave's loads of step s + 1 have landed (later steps may still be in
-      // flight); after the barrier every wave's have, and every wave is done
-      // with step s's buffers.
-      wait_steps(max(0, min(kRingSteps - 2, n_steps - st - 2)));
-      __syncthreads();
     }
 
     // Teams 1.. hand their (m, l, O) to team 0 through LDS (the ring is idle:
@@ -468,10 +461,11 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   }
 }
 
-// LDS of the kernel: the ring of steps (at least the team exchange area).
+// LDS of the kernel: the ring of steps (which also holds the team exchange
+// area), then the page ids of one segment of key tiles.
 template <int kTeams>
 constexpr int prefill_lds_bytes() {
-  return (kTeams == 1 ? 4 : 3) * kTeams * kBufBytes;
+  return (kTeams == 1 ? 4 : 3) * kTeams * kBufBytes + 16 * (kSegTiles + kTeams);
 }
 
 template <int KV, int W, int kTeams>
@@ -480,7 +474,8 @@ int launch_prefill_variant(const dim3 grid, float* out, const float* q, const ui
                            const int32_t* row_seq, const ie_kv_layout& kv, int n_heads,
                            int n_kv_heads, int n_blocks, hipStream_t stream) {
   constexpr int lds = prefill_lds_bytes<kTeams>();
-  static_assert(lds >= W * 4096 + W * 512, "team exchange area must fit in the ring");
+  static_assert(lds - 16 * (kSegTiles + kTeams) >= W * 4096 + W * 512,
+                "team exchange area must fit in the ring");
   if (lds > 65536) {  // above the default dynamic-LDS cap, within gfx950's 160 KB
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(prefill_mfma_kernel<KV, W, kTeams>),
@@ -569,11 +564,19 @@ prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
   const int pos0 = __builtin_amdgcn_readfirstlane(row_pos[0]);
   const int seq = __builtin_amdgcn_readfirstlane(row_seq[0]);
   const int32_t* tab = tables + size_t(seq) * max_pages;
-  auto page_id = [&](const int tile, const int j) -> int {
-    const int pi = tile * (kKeys / IE_HIP_PAGE_SIZE) + j;
-    return pi < max_pages ? tab[pi] : -1;
+  // Page ids of a segment of key tiles staged in LDS after the ring, as in the
+  // 16-bit kernel: ids[4 (tile - seg0) + j], -1 past the table row or outside
+  // the pool.
+  int* const ids = reinterpret_cast<int*>(smem + kRingF32 * kBufF32);
+  int seg0 = 0;
+  auto tile_ids = [&](const int tile) {
+    return *reinterpret_cast<const int4*>(ids + 4 * (tile - seg0));
   };
-  auto valid = [&](const int id) { return id >= 0 && id < num_pages; };
+  auto tile_ok = [&](const int tile) -> int {
+    const int4 v = tile_ids(tile);
+    return __builtin_amdgcn_readfirstlane(int(v.x >= 0) | (int(v.y >= 0) << 1) |
+                                          (int(v.z >= 0) << 2) | (int(v.w >= 0) << 3));
+  };
 
   // DMA of a tile into buffer `buf`: load u (0..15 K, 16..31 V) moves keys
   // 4 (u & 15) .. +3 (page (u & 15) / 4 of the tile); lane l lands at base + 16 l:
@@ -584,8 +587,13 @@ prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
   const unsigned smem_lds = lds_address(smem);
   const char* kbase_g = reinterpret_cast<const char*>(k_pool) + kvh * 256;
   const char* vbase_g = reinterpret_cast<const char*>(v_pool) + kvh * 256;
-  auto issue = [&](const int buf, const int id0, const int id1, const int id2, const int id3) {
+  auto issue = [&](const int buf, const int tile) {
     if (wave >= kDmaWaves) return;
+    const int4 v = tile_ids(tile);
+    const int id0 = max(__builtin_amdgcn_readfirstlane(v.x), 0);
+    const int id1 = max(__builtin_amdgcn_readfirstlane(v.y), 0);
+    const int id2 = max(__builtin_amdgcn_readfirstlane(v.z), 0);
+    const int id3 = max(__builtin_amdgcn_readfirstlane(v.w), 0);
 #pragma unroll
     for (int k = 0; k < kPerWave; ++k) {
       const int u = wave * kPerWave + k;        // 0..31
@@ -596,7 +604,7 @@ prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
       const int key = 4 * uu + lkey;            // key within the tile
       const int piece = is_v ? lslot : (lslot ^ (key & 15));
       const char* src = (is_v ? vbase_g : kbase_g) +
-                        (size_t(valid(id) ? id : 0) * IE_HIP_PAGE_SIZE + (key & 15)) * row_bytes +
+                        (size_t(id) * IE_HIP_PAGE_SIZE + (key & 15)) * row_bytes +
                         16 * piece;
       dma16(src, smem_lds + buf * kBufF32 + (is_v ? kTileF32 : 0) + uu * 1024);
     }
@@ -639,123 +647,118 @@ prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Ring of kRingF32 tiles; page ids read one tile ahead; okq: 4 "page inside
-    // the pool" bits per tile in flight (tile kb in the lowest 4).
-    int nx[4] = {page_id(0, 0), page_id(0, 1), page_id(0, 2), page_id(0, 3)};
-    auto ok_bits = [&]() {
-      return int(valid(nx[0])) | int(valid(nx[1])) << 1 | int(valid(nx[2])) << 2 |
-             int(valid(nx[3])) << 3;
-    };
-    int okq = 0;
-    for (int pre = 0; pre < kRingF32 - 1 && pre < n_tiles; ++pre) {
-      okq |= ok_bits() << (4 * pre);
-      issue(pre, nx[0], nx[1], nx[2], nx[3]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) nx[j] = page_id(pre + 1, j);
-    }
-    wait_tiles(min(kRingF32 - 2, n_tiles - 1));  // tile 0 has landed
-    __syncthreads();
+    // Segments of kSegTiles key tiles, each with its page ids staged in LDS;
+    // within a segment, a ring of kRingF32 tiles.
+    for (seg0 = 0; seg0 < n_tiles; seg0 += kSegTiles) {
+      const int seg_end = min(n_tiles, seg0 + kSegTiles);
+      // The ring is idle and every wave is past its last read of the old ids.
+      for (int i = tid; i < 4 * (seg_end - seg0); i += 64 * kWaves) {
+        const int pi = 4 * seg0 + i;
+        const int id = pi < max_pages ? tab[pi] : -1;
+        ids[i] = id >= 0 && id < num_pages ? id : -1;
+      }
+      __syncthreads();
+      for (int pre = 0; pre < kRingF32 - 1 && seg0 + pre < seg_end; ++pre) issue(pre, seg0 + pre);
+      wait_tiles(min(kRingF32 - 2, seg_end - seg0 - 1));  // the segment's first tile has landed
+      __syncthreads();
 
-    int buf = 0, ibuf = kRingF32 - 1;
-    for (int kb = 0; kb < n_tiles; ++kb) {
-      const int okb = okq & 15;
-      okq >>= 4;
-      const int ahead = kb + kRingF32 - 1;
-      if (ahead < n_tiles) {  // its buffer held tile kb - 1: free since the last barrier
-        okq |= ok_bits() << (4 * (kRingF32 - 2));
-        issue(ibuf, nx[0], nx[1], nx[2], nx[3]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) nx[j] = page_id(ahead + 1, j);
-      }
-      ibuf = ibuf + 1 == kRingF32 ? 0 : ibuf + 1;
-      const int kbase = kb * kKeys;
-      const unsigned char* kt = smem + buf * kBufF32;
-      unsigned char* vt = smem + buf * kBufF32 + kTileF32;
-      buf = buf + 1 == kRingF32 ? 0 : buf + 1;
-      // Keys past max_pos or in pages outside the pool: zero their V rows first.
-      if (kbase + kKeys - 1 > max_pos || okb != 15) {
-        for (int i = tid; i < kKeys * 16; i += 64 * kWaves) {
-          const int key = i >> 4;
-          if (kbase + key > max_pos || !((okb >> (key >> 4)) & 1))
-            *reinterpret_cast<uint4*>(vt + key * 256 + (i & 15) * 16) = make_uint4(0, 0, 0, 0);
+      int buf = 0, ibuf = kRingF32 - 1;
+      for (int kb = seg0; kb < seg_end; ++kb) {
+        const int ahead = kb + kRingF32 - 1;
+        if (ahead < seg_end)  // its buffer held tile kb - 1: free since the last barrier
+          issue(ibuf, ahead);
+        ibuf = ibuf + 1 == kRingF32 ? 0 : ibuf + 1;
+        const int kbase = kb * kKeys;
+        const unsigned char* kt = smem + buf * kBufF32;
+        unsigned char* vt = smem + buf * kBufF32 + kTileF32;
+        buf = buf + 1 == kRingF32 ? 0 : buf + 1;
+        const int okb = tile_ok(kb);
+        // Keys past max_pos or in pages outside the pool: zero their V rows first.
+        if (kbase + kKeys - 1 > max_pos || okb != 15) {
+          for (int i = tid; i < kKeys * 16; i += 64 * kWaves) {
+            const int key = i >> 4;
+            if (kbase + key > max_pos || !((okb >> (key >> 4)) & 1))
+              *reinterpret_cast<uint4*>(vt + key * 256 + (i & 15) * 16) = make_uint4(0, 0, 0, 0);
+          }
+          __syncthreads();
         }
-        __syncthreads();
-      }
-      const float mref = m == -INFINITY ? 0.0f : m;
-      // S^T per key group kt4: A = key 16 kt4 + r, dims 16g + s.
-      f32x4 s[4];
+        const float mref = m == -INFINITY ? 0.0f : m;
+        // S^T per key group kt4: A = key 16 kt4 + r, dims 16g + s.
+        f32x4 s[4];
 #pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4) {
-        const int key = 16 * kt4 + r;
-        float ka[16];
+        for (int kt4 = 0; kt4 < 4; ++kt4) {
+          const int key = 16 * kt4 + r;
+          float ka[16];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float4 x = *reinterpret_cast<const float4*>(kt + key * 256 +
-                                                            16 * ((4 * g + i) ^ (key & 15)));
-          ka[4 * i + 0] = x.x;
-          ka[4 * i + 1] = x.y;
-          ka[4 * i + 2] = x.z;
-          ka[4 * i + 3] = x.w;
+          for (int i = 0; i < 4; ++i) {
+            const float4 x = *reinterpret_cast<const float4*>(kt + key * 256 +
+                                                              16 * ((4 * g + i) ^ (key & 15)));
+            ka[4 * i + 0] = x.x;
+            ka[4 * i + 1] = x.y;
+            ka[4 * i + 2] = x.z;
+            ka[4 * i + 3] = x.w;
+          }
+          f32x4 acc = {-mref, -mref, -mref, -mref};
+#pragma unroll
+          for (int st = 0; st < 16; ++st)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[st], qb[st], acc, 0, 0, 0);
+          s[kt4] = acc;
         }
-        f32x4 acc = {-mref, -mref, -mref, -mref};
+        if (kbase + kKeys - 1 > min_pos || okb != 15) {
 #pragma unroll
-        for (int st = 0; st < 16; ++st)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[st], qb[st], acc, 0, 0, 0);
-        s[kt4] = acc;
-      }
-      if (kbase + kKeys - 1 > min_pos || okb != 15) {
+          for (int kt4 = 0; kt4 < 4; ++kt4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int kp = kbase + 16 * kt4 + 4 * g + e;
+              s[kt4][e] = (kp <= rp && ((okb >> kt4) & 1)) ? s[kt4][e] : -INFINITY;
+            }
+        }
+        // Online softmax on s - mref, the reference max raised lazily (as in the
+        // 16-bit kernel: O and l rescaled only when a row's max grows past
+        // m + kLazyMax somewhere in the wave).
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt4 = 0; kt4 < 4; ++kt4)
+          mx = fmaxf(mx, fmaxf(fmaxf(s[kt4][0], s[kt4][1]), fmaxf(s[kt4][2], s[kt4][3])));
+        mx = group_max4(mx);
+        const bool grow = m == -INFINITY ? mx != -INFINITY : mx > kLazyMax;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float m_new = fmaxf(m, mref + mx);
+          const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m - m_new);  // m = -inf: 0
+          l *= corr;
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) o[mt] *= corr;
+          m = m_new;
+          const float shift = (m_new == -INFINITY ? 0.0f : m_new) - mref;
+#pragma unroll
+          for (int kt4 = 0; kt4 < 4; ++kt4) s[kt4] -= shift;
+        }
+        float sum = 0.0f;
 #pragma unroll
         for (int kt4 = 0; kt4 < 4; ++kt4)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int kp = kbase + 16 * kt4 + 4 * g + e;
-            s[kt4][e] = (kp <= rp && ((okb >> kt4) & 1)) ? s[kt4][e] : -INFINITY;
+            s[kt4][e] = exp2_weight(s[kt4][e]);
+            sum += s[kt4][e];
           }
+        l += sum;
+        // O^T += V^T P^T: step (kt4, e) takes key 16 kt4 + 4g + e; lane (g, r)
+        // reads that key's V piece r (dims 4r .. 4r+3, the 4 tiles' A values).
+#pragma unroll
+        for (int kt4 = 0; kt4 < 4; ++kt4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float4 v =
+                *reinterpret_cast<const float4*>(vt + (16 * kt4 + 4 * g + e) * 256 + 16 * r);
+            const float pw = s[kt4][e];
+            o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, pw, o[0], 0, 0, 0);
+            o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.y, pw, o[1], 0, 0, 0);
+            o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.z, pw, o[2], 0, 0, 0);
+            o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.w, pw, o[3], 0, 0, 0);
+          }
+        wait_tiles(max(0, min(kRingF32 - 2, seg_end - kb - 2)));
+        __syncthreads();
       }
-      // Online softmax on s - mref, the reference max raised lazily (as in the
-      // 16-bit kernel: O and l rescaled only when a row's max grows past
-      // m + kLazyMax somewhere in the wave).
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4)
-        mx = fmaxf(mx, fmaxf(fmaxf(s[kt4][0], s[kt4][1]), fmaxf(s[kt4][2], s[kt4][3])));
-      mx = group_max4(mx);
-      const bool grow = m == -INFINITY ? mx != -INFINITY : mx > kLazyMax;
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float m_new = fmaxf(m, mref + mx);
-        const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m - m_new);  // m = -inf: 0
-        l *= corr;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) o[mt] *= corr;
-        m = m_new;
-        const float shift = (m_new == -INFINITY ? 0.0f : m_new) - mref;
-#pragma unroll
-        for (int kt4 = 0; kt4 < 4; ++kt4) s[kt4] -= shift;
-      }
-      float sum = 0.0f;
-#pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s[kt4][e] = exp2_weight(s[kt4][e]);
-          sum += s[kt4][e];
-        }
-      l += sum;
-      // O^T += V^T P^T: step (kt4, e) takes key 16 kt4 + 4g + e; lane (g, r)
-      // reads that key's V piece r (dims 4r .. 4r+3, the 4 tiles' A values).
-#pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float4 v = *reinterpret_cast<const float4*>(vt + (16 * kt4 + 4 * g + e) * 256 + 16 * r);
-          const float pw = s[kt4][e];
-          o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.x, pw, o[0], 0, 0, 0);
-          o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.y, pw, o[1], 0, 0, 0);
-          o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.z, pw, o[2], 0, 0, 0);
-          o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v.w, pw, o[3], 0, 0, 0);
-        }
-      wait_tiles(max(0, min(kRingF32 - 2, n_tiles - kb - 2)));
-      __syncthreads();
     }
 
     l = group_sum4(l);
@@ -776,7 +779,7 @@ int launch_prefill_f32(const dim3 grid, float* out, const float* q, const float*
                        const float* vp, int T, const int32_t* row_pos, const int32_t* row_seq,
                        const ie_kv_layout& kv, int n_heads, int n_kv_heads, int n_blocks,
                        hipStream_t stream) {
-  constexpr int lds = kRingF32 * kBufF32;  // 96 KB
+  constexpr int lds = kRingF32 * kBufF32 + 16 * kSegTiles;  // 96 KB ring + the segment's page ids
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(prefill_mfma_f32_kernel<W>),
       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
