@@ -149,13 +149,17 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   unsigned char* warea = smem + size_t(wave) * kTile;
   const unsigned warea_lds = lds_address(smem) + wave * kTile;
 
-  // Page id of the wave's page `pw` (uniform, scalar load); -1 past the wave's
-  // positions or the table row.
+  // Page ids of the wave's pages, one per lane (lane i: page i of the wave's
+  // positions; -1 past them or past the table row), loaded once. A pair's ids
+  // are read from this register (readlane): a scalar load of the table inside
+  // the pair loop would share lgkmcnt with the transposed V reads, so the
+  // first V wait of every pair would also wait for the table's round trip.
+  // A wave covers at most 32 pages (the host keeps it to 512 positions).
   const int pi0 = (s0 + wt0) / IE_HIP_PAGE_SIZE;
   const int32_t* row_tab = tables + size_t(seq) * max_pages;
+  const int pid_lane = (16 * lane < nw && pi0 + lane < max_pages) ? row_tab[pi0 + lane] : -1;
   auto page_id = [&](const int pw) -> int {
-    const int pi = pi0 + pw;
-    return (16 * pw < nw && pi < max_pages) ? row_tab[pi] : -1;
+    return pw < 64 ? __builtin_amdgcn_readlane(pid_lane, pw) : -1;
   };
 
   // The query of head r (the B operand's column), dims [8g, 8g+8) and
@@ -543,11 +547,14 @@ decode_partial_mfma_f32(float* __restrict__ out, float* __restrict__ part_o,
   const int n = min(s0 + chunk_tokens, p + 1) - s0;  // positions of this chunk
   const bool single = s0 == 0 && p < chunk_tokens;  // the row fits this one chunk
   const int npg = (n + IE_HIP_PAGE_SIZE - 1) / IE_HIP_PAGE_SIZE;
+  // Page ids of the chunk (at most 64 pages), one per lane, loaded once and read
+  // per page with readlane (no table load waits inside the page loop), as in
+  // the 16-bit kernel.
   const int pi0 = s0 / IE_HIP_PAGE_SIZE;
   const int32_t* row_tab = tables + size_t(seq) * max_pages;
+  const int pid_lane = (16 * lane < n && pi0 + lane < max_pages) ? row_tab[pi0 + lane] : -1;
   auto page_id = [&](const int pw) -> int {
-    const int pi = pi0 + pw;
-    return (16 * pw < n && pi < max_pages) ? row_tab[pi] : -1;
+    return pw < 64 ? __builtin_amdgcn_readlane(pid_lane, pw) : -1;
   };
   auto valid = [&](const int id) { return id >= 0 && id < num_pages; };
 
@@ -717,6 +724,8 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
   const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
   const int waves = decode_mfma_waves(chunk_tokens, slots);
   const size_t lds = size_t(waves) * kTile;
+  if (chunk_tokens / waves > 512)  // a wave's page ids live one per lane
+    return fail(IE_HIP_EINVAL, "attention: more than 512 positions per wave");
   if (slots * n_heads * 64 * 4 > 0x7fffffff)
     return fail(IE_HIP_EINVAL, "attention: split-K workspace above 2 GB (too many rows x chunks)");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
