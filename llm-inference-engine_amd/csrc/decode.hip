@@ -75,7 +75,7 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
   for (int i = tid; i < (n + IE_HIP_PAGE_SIZE - 1) / IE_HIP_PAGE_SIZE; i += kThreads) {
     const int pi = s0 / IE_HIP_PAGE_SIZE + i;
     const int page = pi < max_pages ? tables[size_t(seq) * max_pages + pi] : -1;
-    pages_s[i] = (page >= 0 && page < num_pages) ? page : 0;
+    pages_s[i] = (page >= 0 && page < num_pages) ? page : -1;  // -1: outside the pool, skipped
   }
   for (int i = tid; i < G * HD; i += kThreads)
     q_s[i / HD][i % HD] = q[(size_t(t) * n_heads + h0) * HD + i];
@@ -86,9 +86,14 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
 #pragma unroll
   for (int g = 0; g < G; ++g) mx[g] = -INFINITY;
   for (int tl = tid; tl < n; tl += kThreads) {
+    const int page = pages_s[tl / IE_HIP_PAGE_SIZE];
+    if (page < 0) {  // a page outside the pool: its positions are not attended
+#pragma unroll
+      for (int g = 0; g < G; ++g) scores[g * chunk_tokens + tl] = -INFINITY;
+      continue;
+    }
     const typename K::elem* kr =
-        k_pool + (size_t(pages_s[tl / IE_HIP_PAGE_SIZE]) * IE_HIP_PAGE_SIZE + tl % IE_HIP_PAGE_SIZE) *
-                     kv_dim + kvh * HD;
+        k_pool + (size_t(page) * IE_HIP_PAGE_SIZE + tl % IE_HIP_PAGE_SIZE) * kv_dim + kvh * HD;
     float kk[HD];
 #pragma unroll
     for (int d8 = 0; d8 < HD / 8; ++d8) K::load8(kr + 8 * d8, kk + 8 * d8);
@@ -138,7 +143,8 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
   for (int tl = tid; tl < n; tl += kThreads) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float e = expf(scores[g * chunk_tokens + tl] - M[g]);
+      // M = -inf: every position of the chunk was skipped; its weights are 0.
+      const float e = M[g] == -INFINITY ? 0.0f : expf(scores[g * chunk_tokens + tl] - M[g]);
       scores[g * chunk_tokens + tl] = e;
       ls[g] += e;
     }
@@ -166,9 +172,11 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
     for (int u = 0; u < 8; ++u) acc[g][u] = 0.0f;
 #pragma unroll 2
   for (int tl = wave * 8 + pg; tl < n; tl += kWaves * 8) {
+    const int page = pages_s[tl / IE_HIP_PAGE_SIZE];
+    if (page < 0) continue;  // skipped position (weight 0; its memory is never read)
     const typename K::elem* vr =
-        v_pool + (size_t(pages_s[tl / IE_HIP_PAGE_SIZE]) * IE_HIP_PAGE_SIZE + tl % IE_HIP_PAGE_SIZE) *
-                     kv_dim + kvh * HD + ds * 8;
+        v_pool + (size_t(page) * IE_HIP_PAGE_SIZE + tl % IE_HIP_PAGE_SIZE) * kv_dim + kvh * HD +
+        ds * 8;
     float vv[8];
     K::load8(vr, vv);
 #pragma unroll

@@ -38,6 +38,7 @@ prefill_valu(float* __restrict__ out, const float* __restrict__ q,
   static_assert(HD == 64, "8 threads x 8 elements stage one 64-wide row");
   __shared__ __align__(16) float ks[kPfKeys][HD];
   __shared__ __align__(16) float vs[kPfKeys][HD];
+  __shared__ int kvis[kPfKeys];  // key j of the tile exists: at most max_pos, page in the pool
   const int group = n_heads / n_kv_heads;
   const int kvh = blockIdx.y, t0 = blockIdx.x * kPfRows;
   const int tid = threadIdx.x, qi = tid / kPfSlots, g = tid % kPfSlots;
@@ -69,16 +70,19 @@ prefill_valu(float* __restrict__ out, const float* __restrict__ q,
       const int j = tid / 8, d8 = (tid % 8) * 8;
       const int s = s0 + j;
       float kx[8] = {0, 0, 0, 0, 0, 0, 0, 0}, vx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      bool vis = false;
       if (s <= max_pos) {
         const int pi = s / IE_HIP_PAGE_SIZE;
         const int page = pi < max_pages ? tables[size_t(seq) * max_pages + pi] : -1;
-        if (page >= 0 && page < num_pages) {
+        if (page >= 0 && page < num_pages) {  // a page outside the pool is not attended
           const size_t off = (size_t(page) * IE_HIP_PAGE_SIZE + s % IE_HIP_PAGE_SIZE) * kv_dim +
                              size_t(kvh) * HD + d8;
           K::load8(k_pool + off, kx);
           K::load8(v_pool + off, vx);
+          vis = true;
         }
       }
+      if (d8 == 0) kvis[j] = vis;
       *reinterpret_cast<float4*>(&ks[j][d8]) = make_float4(kx[0], kx[1], kx[2], kx[3]);
       *reinterpret_cast<float4*>(&ks[j][d8 + 4]) = make_float4(kx[4], kx[5], kx[6], kx[7]);
       *reinterpret_cast<float4*>(&vs[j][d8]) = make_float4(vx[0], vx[1], vx[2], vx[3]);
@@ -99,7 +103,7 @@ prefill_valu(float* __restrict__ out, const float* __restrict__ q,
         dot = __builtin_fmaf(qr[d + 2], kk.z, dot);
         dot = __builtin_fmaf(qr[d + 3], kk.w, dot);
       }
-      sc[j] = (s0 + j <= pos) ? dot : -INFINITY;
+      sc[j] = (s0 + j <= pos && kvis[j]) ? dot : -INFINITY;
       tile_max = fmaxf(tile_max, sc[j]);
     }
     const float m_new = fmaxf(m, tile_max);

@@ -303,3 +303,44 @@ def test_stale_nonfinite_pool_rows_do_not_leak(ie, O, dev, kv, impl):
     for ct in (64, 128, 256):
         got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct)
         check(O, got, want, kvt, f"chunk {ct}")
+
+
+@pytest.mark.parametrize("kv", list(KVS))
+def test_out_of_pool_pages_are_skipped(ie, O, dev, kv, impl):
+    """Table entries outside the pool (past it or negative) inside rows' contexts: the
+    kernels never dereference them and their positions are not attended, while every
+    pool row the attention may not see holds inf/NaN. Cases: two pages in the middle
+    of a row; the row's first page; its last page (its own position among the
+    skipped ones); a whole 128-position chunk (an all-skipped partial in the merge).
+    Expected: per row, the oracle's attention over the sequence with the skipped
+    positions removed, where the row's query sits at the last kept position <= p."""
+    kvt = KVS[kv]
+    rng = np.random.default_rng(47)
+    lens = [700, 100, 300, 700]
+    tables, max_pages, num_pages = make_tables(lens, rng, extra_pages=3)
+    good = tables.copy()
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    used = np.zeros(num_pages * 16, bool)
+    for s_, n in enumerate(lens):
+        for p_ in range(n):
+            used[good[s_, p_ // 16] * 16 + p_ % 16] = True
+    poison = O.round_to_kv(np.resize(np.array([np.nan, np.inf], np.float32),
+                                     (int((~used).sum()), KVD)).astype(np.float32), kvt)
+    kp[~used] = poison
+    vp[~used] = poison
+    skipped = {0: [5, 6], 1: [0], 2: [18], 3: list(range(8, 16))}
+    for s_, pages in skipped.items():
+        for i, pg in enumerate(pages):
+            tables[s_, pg] = num_pages + 5 if i % 2 == 0 else -2
+    row_pos = np.array([n - 1 for n in lens], np.int32)
+    row_seq = np.arange(len(lens), dtype=np.int32)
+    q = normal(rng, (len(lens), QD))
+    want = np.empty_like(q)
+    for s_, n in enumerate(lens):
+        keep = np.array([p_ for p_ in range(n) if p_ // 16 not in skipped[s_]])
+        kc = O.gather_kv(kp, kvt, good, max_pages, s_, n, KVD)[keep]
+        vc = O.gather_kv(vp, kvt, good, max_pages, s_, n, KVD)[keep]
+        want[s_] = O.attention(q[s_:s_ + 1], kc, vc, len(keep) - 1, NH, NKV, HD)[0]
+    for ct in (64, 128, 256):
+        got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct)
+        check(O, got, want, kvt, f"chunk {ct}")

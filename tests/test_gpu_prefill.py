@@ -154,3 +154,37 @@ def test_stale_nonfinite_pool_rows_do_not_leak(ie, O, dev, kv, impl):
     want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD)
     check(O, gpu_prefill(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages), want, kvt,
           "stale rows")
+
+
+@pytest.mark.parametrize("kv", list(KVS))
+def test_out_of_pool_pages_are_skipped(ie, O, dev, kv, impl):
+    """Table entries outside the pool (one past it, one negative) inside a prompt's
+    context: the kernels never dereference them and their 32 keys are invisible
+    (scores masked, V elements zeroed), while every other byte of the pool holds
+    inf/NaN. Expected: the oracle's attention over the sequence with those 32
+    positions removed -- rows at positions p >= 48 then see the first p + 1 - 32
+    keys of the compacted copy, i.e. position p - 32 of it."""
+    kvt = KVS[kv]
+    rng = np.random.default_rng(46)
+    L, start = 300, 100
+    tables, max_pages, num_pages = make_tables([L], rng, extra_pages=2)
+    good = tables.copy()
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    used = np.zeros(num_pages * 16, bool)
+    for p_ in range(L):
+        used[good[0, p_ // 16] * 16 + p_ % 16] = True
+    poison = O.round_to_kv(np.resize(np.array([np.inf, np.nan], np.float32),
+                                     (int((~used).sum()), KVD)).astype(np.float32), kvt)
+    kp[~used] = poison
+    vp[~used] = poison
+    tables[0, 1] = num_pages + 7  # positions 16..31
+    tables[0, 2] = -3             # positions 32..47
+    row_pos = np.arange(start, L, dtype=np.int32)
+    row_seq = np.zeros(len(row_pos), np.int32)
+    q = normal(rng, (len(row_pos), QD))
+    keep = np.r_[0:16, 48:L]
+    kc = O.gather_kv(kp, kvt, good, max_pages, 0, L, KVD)[keep]
+    vc = O.gather_kv(vp, kvt, good, max_pages, 0, L, KVD)[keep]
+    want = O.attention(q, kc, vc, start - 32, NH, NKV, HD, threads=8)
+    check(O, gpu_prefill(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages), want, kvt,
+          "out-of-pool pages")
