@@ -107,15 +107,13 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   // page 0 and masked). A step then reads its tiles' ids from LDS instead of
   // the table: no memory round trip inside the tile loop.
   int* const ids = reinterpret_cast<int*>(smem + kRingBytes);
+  // Per step of the segment, staged after the ids: bits 4 tm .. 4 tm + 3 = the
+  // in-pool bits of team tm's tile, bit 8 = some tile of the step needs V rows
+  // zeroed (past max_pos or a page outside the pool). One LDS read per step.
+  int* const step_flags = ids + 4 * (kSegTiles + kTeams);
   int seg0 = 0;  // first tile of the segment in progress
   auto tile_ids = [&](const int tile) {
     return *reinterpret_cast<const int4*>(ids + 4 * (tile - seg0));
-  };
-  // Bit j set: page j of the tile is inside the pool (uniform).
-  auto tile_ok = [&](const int tile) -> int {
-    const int4 v = tile_ids(tile);
-    return __builtin_amdgcn_readfirstlane(int(v.x >= 0) | (int(v.y >= 0) << 1) |
-                                          (int(v.z >= 0) << 2) | (int(v.w >= 0) << 3));
   };
   // Buffer of the tile a team takes at step s.
   auto buffer = [&](const int ring_step, const int tm) { return ring_step * kTeams + tm; };
@@ -245,6 +243,19 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
         ids[i] = id >= 0 && id < num_pages ? id : -1;
       }
       __syncthreads();
+      for (int i = tid; i < n_steps; i += 64 * kWaves * kTeams) {
+        int f = 0;
+#pragma unroll
+        for (int tm = 0; tm < kTeams; ++tm) {
+          const int tile = seg0 + kTeams * i + tm;
+          const int4 v = tile_ids(tile);
+          const int ok = int(v.x >= 0) | (int(v.y >= 0) << 1) | (int(v.z >= 0) << 2) |
+                         (int(v.w >= 0) << 3);
+          f |= ok << (4 * tm);
+          if (tile < n_tiles && (tile * kKeys + kKeys - 1 > max_pos || ok != 15)) f |= 1 << 8;
+        }
+        step_flags[i] = f;
+      }  // read after the barrier below
       for (int pre = 0; pre < kRingSteps - 1 && pre < n_steps; ++pre)
         issue(buffer(pre, team), seg0 + kTeams * pre + team);
       wait_steps(min(kRingSteps - 2, n_steps - 1));  // step 0 has landed
@@ -253,6 +264,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       int rs = 0;               // ring slot of step s
       int is = kRingSteps - 1;  // ring slot of step s + kRingSteps - 1
       for (int st = 0; st < n_steps; ++st) {
+        const int fl = __builtin_amdgcn_readfirstlane(step_flags[st]);  // read with the ids below
         const int ahead = st + kRingSteps - 1;
         if (ahead < n_steps)  // its buffers held step s - 1: free since the last barrier
           issue(buffer(is, team), seg0 + kTeams * ahead + team);
@@ -266,14 +278,8 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
         // Keys past max_pos (the last tile) or in pages outside the pool: zero
         // their V rows before the team reads the tile. The decision covers every
         // tile of the step, so every wave takes the same branch and barrier.
-        bool zero_step = false;
-#pragma unroll
-        for (int tm = 0; tm < kTeams; ++tm) {
-          const int tile = seg0 + kTeams * st + tm;
-          if (tile < n_tiles)
-            zero_step |= tile * kKeys + kKeys - 1 > max_pos || tile_ok(tile) != 15;
-        }
-        const int okb = kb < n_tiles ? tile_ok(kb) : 0;
+        const bool zero_step = (fl >> 8) & 1;
+        const int okb = (fl >> (4 * team)) & 15;
         if (zero_step) {
           if (kb < n_tiles) {
             for (int i = tid - 64 * kWaves * team; i < kKeys * 8; i += 64 * kWaves) {
@@ -465,7 +471,8 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
 // area), then the page ids of one segment of key tiles.
 template <int kTeams>
 constexpr int prefill_lds_bytes() {
-  return (kTeams == 1 ? 4 : 3) * kTeams * kBufBytes + 16 * (kSegTiles + kTeams);
+  return (kTeams == 1 ? 4 : 3) * kTeams * kBufBytes + 16 * (kSegTiles + kTeams) +
+         4 * kSegTiles;
 }
 
 template <int KV, int W, int kTeams>
@@ -474,7 +481,7 @@ int launch_prefill_variant(const dim3 grid, float* out, const float* q, const ui
                            const int32_t* row_seq, const ie_kv_layout& kv, int n_heads,
                            int n_kv_heads, int n_blocks, hipStream_t stream) {
   constexpr int lds = prefill_lds_bytes<kTeams>();
-  static_assert(lds - 16 * (kSegTiles + kTeams) >= W * 4096 + W * 512,
+  static_assert(lds - 16 * (kSegTiles + kTeams) - 4 * kSegTiles >= W * 4096 + W * 512,
                 "team exchange area must fit in the ring");
   if (lds > 65536) {  // above the default dynamic-LDS cap, within gfx950's 160 KB
     static const hipError_t attr = hipFuncSetAttribute(
