@@ -11,7 +11,13 @@ Each step reads a different layer's pools (--layers, default 8 x 537 MB), so
 the >= 2 x 256 MB working set defeats the 256 MB Infinity Cache and the rate
 is HBM, not MALL. value = algorithmic bytes / time (GB/s):
     per row  512*L (K+V, f16) + 3584 (q) + 3584 (out) + 4*ceil(L/16) (page ids) + 8
-The roofline fraction is against the nominal 8 TB/s. cpu_baseline times the
+The roofline fraction is against the nominal 8 TB/s. Its duration (us_per_launch) is
+the graph-timed time per entry-point call: every kernel the call launches (named in
+roofline.kernel; for attention the partial kernel and the split-K merge) and the launch
+gaps between calls. The rocprofv3 kernel trace under profiles/ gives each kernel's own
+average; they add up to this figure less the gaps. Bracketing one kernel with HIP events
+was tried and dropped: event records around a launch slowed the kernel itself (the
+prefill 71 -> 86 us). cpu_baseline times the
 reference's own CPU attention (oracle/_ref: src/ops.cpp + src/threadpool.cpp,
 -O3 -mavx2 -mfma) on the same batch, rows gathered to contiguous fp32 first
 (gather timed separately), on this host's cores.
@@ -207,7 +213,10 @@ def bench_decode(args, torch, ie, O):
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles("decode", kv, "f16", args)},
+                     "traffic": traffic_from_profiles("decode", kv, "f16", args),
+                     "kernel": ("decode_partial_mfma_f32" if kv == "f32" else "decode_partial_mfma")
+                               + " + decode_merge_kernel (one ie_hip_attention call)",
+                     "us_per_launch": round(ms * 1e3, 3)},
         "algorithmic_bytes_per_step": nbytes,
         "warm_mall": {"ms_per_step": round(ms_warm, 5),
                       "gbs": round(nbytes / (ms_warm * 1e-3) / 1e9, 2),
@@ -267,7 +276,9 @@ def bench_append(args, torch, ie, O):
                                "65,536-page pool", "kv_dtype": kv, "seed": args.seed},
         "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 5),
-                     "traffic": traffic_from_profiles("append", kv, "f16", args)},
+                     "traffic": traffic_from_profiles("append", kv, "f16", args),
+                     "kernel": "rope_append_kernel (one ie_hip_rope_and_cache call)",
+                     "us_per_launch": head["us_per_launch"]},
         "sweep": sweep,
     }
 
@@ -334,7 +345,11 @@ def bench_long(args, torch, ie, O):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles("long" if fused else "long_unfused",
-                                                      kv, "bf16", args)},
+                                                      kv, "bf16", args),
+                     "kernel": "24 x (decode_partial_mfma + decode_merge_kernel)" if fused
+                               else "24 x (rope_append_kernel + decode_partial_mfma + "
+                                    "decode_merge_kernel)",
+                     "us_per_launch": round(ms * 1e3, 3)},
         "algorithmic_bytes_per_step": nbytes,
     }
 
@@ -425,7 +440,10 @@ def bench_mixed(args, torch, ie, O):
         "decode_part_gbs": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": mfma_peak,
                      "unit": "TFLOP/s", "frac": round(tflops / mfma_peak, 4), "traffic": None,
-                     "kernel": "attention_prefill (causal 4,000 x 4,000, 28.7 GFLOP)"},
+                     "kernel": ("prefill_mfma_f32_kernel" if kv == "f32" else "prefill_mfma_kernel")
+                               + " (one ie_hip_attention_prefill call, causal 4,000 x 4,000, "
+                                 "28.7 GFLOP)",
+                     "us_per_launch": round(ms_pf * 1e3, 3)},
     }
 
 
