@@ -31,6 +31,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -158,6 +159,114 @@ def cpu_baseline_decode(O, lens, k_host, v_host, tables, kv, q_host, budget_s=10
     }
 
 
+def _cpu_threads(O):
+    cores = min(O.physical_cores(), NH)  # the reference splits attention over heads only
+    if O.ref_available():
+        O.ref().ref_set_num_threads(cores)
+    return cores
+
+
+def _ref_attention(O, q, k, v, pos0, cores):
+    if O.ref_available():
+        return O.ref_attention(q, k, v, pos0, NH, NKV, HD)
+    return O.attention(q, k, v, pos0, NH, NKV, HD, threads=cores)
+
+
+def cpu_baseline_append(O, q, k, v, pos, kv, budget_s=3.0):
+    """Config 2 on the CPU: RoPE of q and k and the paged K/V write for the 64 rows, the
+    oracle's restatement of the reference's rope + append (src/ops.cpp:34-55,
+    src/model.cpp:70-75) in one C call per batch, into a compact pool holding the
+    rows' pages (the write pattern is the same)."""
+    T = len(pos)
+    pos = np.ascontiguousarray(pos, np.int32)
+    pi = pos.astype(np.int64) // PAGE
+    max_pages = int(pi.max()) + 1
+    tables = np.zeros((T, max_pages), np.int32)
+    tables[np.arange(T), pi] = np.arange(T)  # row t's page is page t of the compact pool
+    seqs = np.arange(T, dtype=np.int32)
+    kvn = O.KV_NP[KV_CODES[kv]]
+    kp = np.zeros((T * PAGE, KVD), kvn)
+    vp = np.zeros((T * PAGE, KVD), kvn)
+    lib = O.orc()
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    times, t_start = [], time.perf_counter()
+    while True:
+        qq = np.ascontiguousarray(q, np.float32).copy()
+        t0 = time.perf_counter()
+        lib.orc_rope_append_paged(ptr(qq), ptr(k), ptr(v), ptr(kp), ptr(vp), KV_CODES[kv], T,
+                                  ptr(pos), ptr(seqs), ptr(tables), max_pages, PAGE, NH, NKV, HD,
+                                  ctypes.c_float(THETA))
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start >= budget_s:
+            break
+    t = float(np.median(times))
+    per_row = 1024 + 2 * KVD * KV_BYTES[kv] + 8 + 4 + 2 * QD * 4
+    return {"value": round(T * per_row / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"the 64 rows with q, {len(times)} batches; median {t * 1e6:.1f} us per batch "
+                      f"(oracle/oracle.cpp, single thread, as the reference's rope runs)",
+            "us_per_launch": round(t * 1e6, 2)}
+
+
+def cpu_baseline_long(O, k_pools, v_pools, tabs, q, L, kv, layers, budget_s=8.0):
+    """Config 4 on the CPU: per layer, the 32k-position row gathered to contiguous fp32
+    (the self-test method, src/cuda/cuda_runner.cu:959-965; timed apart) and the
+    reference's attention over it, on as many layers as the budget allows; the step
+    time is the median layer time x 24."""
+    cores = _cpu_threads(O)
+    attn, gath, t_start, n = [], [], time.perf_counter(), 0
+    while True:
+        l = n % len(k_pools)
+        t0 = time.perf_counter()
+        idx = tabs[l][0, np.arange(L) // PAGE].astype(np.int64) * PAGE + np.arange(L) % PAGE
+        kc = O.widen_kv(k_pools[l][idx], KV_CODES[kv]) if kv != "f32" else k_pools[l][idx]
+        vc = O.widen_kv(v_pools[l][idx], KV_CODES[kv]) if kv != "f32" else v_pools[l][idx]
+        t1 = time.perf_counter()
+        _ref_attention(O, q[l], kc, vc, L - 1, cores)
+        attn.append(time.perf_counter() - t1)
+        gath.append(t1 - t0)
+        n += 1
+        if time.perf_counter() - t_start >= budget_s and n >= 2:
+            break
+    t = float(np.median(attn)) * layers
+    per_layer = 2 * KVD * KV_BYTES[kv] * L + 2 * QD * 4 + 4 * (L // PAGE) + 8
+    return {"value": round(layers * per_layer / t / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "reference" if O.ref_available() else "port",
+            "sample": f"{n} layers' attention over 32,768 positions (gather to contiguous fp32 "
+                      f"excluded, median {float(np.median(gath)) * 1e3:.1f} ms); step = median "
+                      f"layer x {layers}",
+            "ms_per_step": round(t * 1e3, 2), "tok_per_s": round(1 / t, 2)}
+
+
+def cpu_baseline_mixed(O, pq_h, kc_pf, vc_pf, P, dq_h, dec_kv, budget_s=10.0):
+    """Config 5 on the CPU: the reference's attention for the prompt's last rows (scaled
+    to all 4,000 rows by their causal flop count) and for the 48 decode rows over
+    their gathered contexts."""
+    cores = _cpu_threads(O)
+    sub = 400  # prompt rows timed: positions P - sub .. P - 1
+    pf, dc, t_start = [], [], time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        _ref_attention(O, pq_h[P - sub:], kc_pf, vc_pf, P - sub, cores)
+        t1 = time.perf_counter()
+        for r, (kc, vc) in enumerate(dec_kv):
+            _ref_attention(O, dq_h[r], kc, vc, len(kc) - 1, cores)
+        t2 = time.perf_counter()
+        pf.append(t1 - t0)
+        dc.append(t2 - t1)
+        if time.perf_counter() - t_start >= budget_s:
+            break
+    flops_sub = 4 * NH * HD * sum(p + 1 for p in range(P - sub, P))
+    flops_all = 4 * NH * HD * P * (P + 1) // 2
+    t_pf = float(np.median(pf)) * flops_all / flops_sub
+    t = t_pf + float(np.median(dc))
+    return {"value": round((len(dec_kv) + P) / t, 1), "unit": "rows/s", "cores": cores,
+            "kind": "reference" if O.ref_available() else "port",
+            "sample": f"prompt rows {P - sub}..{P - 1} ({len(pf)} passes, scaled to the 4,000-row "
+                      f"prefill by causal flops) + the 48 decode rows; gathers excluded",
+            "prefill_s": round(t_pf, 4), "prefill_tflops": round(flops_all / t_pf / 1e12, 4),
+            "decode_ms": round(float(np.median(dc)) * 1e3, 3)}
+
+
 def bench_decode(args, torch, ie, O):
     dev = torch.device("cuda:0")
     kv = args.kv or "f16"
@@ -257,6 +366,8 @@ def bench_append(args, torch, ie, O):
         q = torch.randn((rows, QD), generator=gen, device=dev)
         k = torch.randn((rows, KVD), generator=gen, device=dev)
         v = torch.randn((rows, KVD), generator=gen, device=dev)
+        if rows == 64:
+            cpu_in = (q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), pos.copy())
         for with_q in (False, True):
             def step(i):
                 ie.rope_and_cache(q if with_q else None, k, v, k_pool, v_pool, table, d_pos, d_seq,
@@ -266,7 +377,7 @@ def bench_append(args, torch, ie, O):
             sweep.append({"rows": rows, "with_q": with_q, "us_per_launch": round(ms * 1e3, 3),
                           "gbs": round(rows * per_row / (ms * 1e-3) / 1e9, 2)})
     head = [s for s in sweep if s["rows"] == 64 and not s["with_q"]][0]
-    return {
+    res = {
         "metric": "paged RoPE+KV append GB/s at batch 64 (K/V only), 1 GPU",
         "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(head["us_per_launch"] / 1e3, 6),
@@ -281,6 +392,9 @@ def bench_append(args, torch, ie, O):
                      "us_per_launch": head["us_per_launch"]},
         "sweep": sweep,
     }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_append(O, *cpu_in, kv)
+    return res
 
 
 def bench_long(args, torch, ie, O):
@@ -331,7 +445,7 @@ def bench_long(args, torch, ie, O):
         (1024 + 2 * KVD * KV_BYTES[kv] + 12 + 2 * QD * 4)
     nbytes = layers * per_layer
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {
+    res = {
         "metric": "long-context decode step (24 layers, batch 1, 32k context) GB/s, 1 GPU",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
@@ -352,6 +466,15 @@ def bench_long(args, torch, ie, O):
                      "us_per_launch": round(ms * 1e3, 3)},
         "algorithmic_bytes_per_step": nbytes,
     }
+    if not args.no_cpu:
+        n_cpu = 3  # layers copied to the host for the CPU sample
+        host = lambda t: (t.cpu().numpy() if kv == "f32" else
+                          t.cpu().view(torch.int16).numpy().view(np.uint16))
+        res["cpu_baseline"] = cpu_baseline_long(
+            O, [host(k_pools[l]) for l in range(n_cpu)], [host(v_pools[l]) for l in range(n_cpu)],
+            [tabs[l].cpu().numpy() for l in range(n_cpu)], [q[l].cpu().numpy() for l in range(n_cpu)],
+            L, kv, layers)
+    return res
 
 
 def bench_mixed(args, torch, ie, O):
@@ -425,7 +548,7 @@ def bench_mixed(args, torch, ie, O):
     mfma_peak = 157.3 if kv == "f32" else 2500.0
     tflops = flops / (ms_pf * 1e-3) / 1e12
     dec_bytes = decode_bytes([lens[s] + 1 for s in dec], KV_BYTES[kv])
-    return {
+    res = {
         "metric": "mixed serving step (48 decode rows + 4,000-token prefill, one layer), 1 GPU",
         "value": round((n_dec + P) / (ms * 1e-3), 1), "unit": "rows/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
@@ -445,6 +568,24 @@ def bench_mixed(args, torch, ie, O):
                                  "28.7 GFLOP)",
                      "us_per_launch": round(ms_pf * 1e3, 3)},
     }
+    if not args.no_cpu:
+        host = lambda t: (t.cpu().numpy() if kv == "f32" else
+                          t.cpu().view(torch.int16).numpy().view(np.uint16))
+        kh, vh = host(k_pool), host(v_pool)
+        tab_h = d_tab.cpu().numpy().reshape(pool.max_batch, max_pages)
+
+        def gather(sq, n):  # the sequence's positions 0..n-1, contiguous fp32
+            idx = tab_h[sq, np.arange(n) // PAGE].astype(np.int64) * PAGE + np.arange(n) % PAGE
+            kc, vc = kh[idx], vh[idx]
+            if kv != "f32":
+                kc, vc = O.widen_kv(kc, KV_CODES[kv]), O.widen_kv(vc, KV_CODES[kv])
+            return np.ascontiguousarray(kc, np.float32), np.ascontiguousarray(vc, np.float32)
+
+        kc_pf, vc_pf = gather(pf, P)
+        res["cpu_baseline"] = cpu_baseline_mixed(O, pq.cpu().numpy(), kc_pf, vc_pf, P,
+                                                 dq.cpu().numpy(),
+                                                 [gather(sq, lens[sq] + 1) for sq in dec])
+    return res
 
 
 def traffic_from_profiles(key: str, kv: str, default_kv: str, args):
