@@ -344,3 +344,62 @@ def test_out_of_pool_pages_are_skipped(ie, O, dev, kv, impl):
     for ct in (64, 128, 256):
         got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct)
         check(O, got, want, kvt, f"chunk {ct}")
+
+
+BATCH_SHAPES = [
+    # rows, context length range [lo, hi), chunk tokens (None: the library's choice)
+    (64, (128, 4097), None),  # BASELINE config 3's shape (128-token chunks)
+    (64, (1, 300), 64),
+    (200, (1, 2000), 128),
+    (256, (1, 700), 64),
+    (257, (1, 700), 64),
+    (3, (1, 5000), 64),
+    (1, (2000, 2001), 64),
+    (40, (1, 40), 64),        # every row inside its first chunk
+]
+
+
+@pytest.mark.parametrize("case", range(len(BATCH_SHAPES)))
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_batch_shapes(ie, O, dev, case, kv):
+    """Batches of 1 to 257 rows of random lengths with one-wave and four-wave chunk
+    workgroups. Rows with position -1 take no work and their output is left as it was; a
+    row past the chunks' capacity (num_chunks * chunk_tokens positions) attends to that
+    many (expected: the oracle at the last covered position). A second call on the same
+    workspace, with other lengths, must not read the first call's partials."""
+    T, (lo, hi), ct = BATCH_SHAPES[case]
+    kvt = KVS[kv]
+    rng = np.random.default_rng(900 + case)
+    lens = rng.integers(lo, hi, T)
+    tables, max_pages, num_pages = make_tables(lens, rng, extra_pages=3)
+    max_pages = int(max_pages)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_seq = np.arange(T, dtype=np.int32)
+    if ct is None:
+        ct = ie.attention_chunk_tokens(T, int(lens.max()), kvt)
+    nc = ie.attention_chunks(int(lens.max()), ct)
+    ws = ie.attention_workspace(T, NH, HD, nc)
+    d_kp, d_vp, d_tab = to_dev(kp, dev, kvt), to_dev(vp, dev, kvt), to_dev(tables, dev)
+    d_seq = to_dev(row_seq, dev)
+    for call in range(2):
+        pos = (lens - 1).astype(np.int32)
+        if call == 1:  # shorter contexts: other chunk counts per row
+            pos = (rng.integers(1, lens + 1) - 1).astype(np.int32)
+        empty = rng.random(T) < (0.1 if T > 4 else 0.0)
+        pos[empty] = -1
+        capped = None
+        if T >= 40 and call == 0:  # one row past the capacity of nc - 1 chunks
+            capped = int(np.argmax(np.where(empty, -1, pos)))
+        ncall = nc - 1 if capped is not None and nc > 1 and pos[capped] >= (nc - 1) * ct else nc
+        q = normal(rng, (T, QD))
+        eff = np.minimum(pos, ncall * ct - 1).astype(np.int32)
+        live = pos >= 0
+        want = O.paged_attention(q[live], kp, vp, kvt, eff[live], row_seq[live], tables,
+                                 max_pages, NH, NKV, HD, threads=8)
+        out = torch.full((T, QD), 7.0, dtype=torch.float32, device=dev)
+        ie.attention(out, to_dev(q, dev), d_kp, d_vp, to_dev(pos, dev), d_seq, d_tab, max_pages,
+                     ncall, ct, ws, NH, NKV, HD)
+        torch.cuda.synchronize()
+        got = from_dev(out)
+        check(O, got[live], want, kvt, f"call {call}, chunk {ct}, {ncall} chunks")
+        assert np.all(got[~live] == 7.0), "rows with position -1 must be left untouched"
