@@ -243,3 +243,105 @@ def compare(got, want):
     rel = orc().orc_compare(_ptr(g), _ptr(w), ctypes.c_size_t(w.size), ctypes.byref(mae),
                             ctypes.byref(worst))
     return float(rel), float(mae.value), int(worst.value)
+
+
+# ------------------------------------------------ the decode step's layer ----
+W_F32, W_BF16, W_I8 = 0, 1, 2  # weight formats (src/matrix.h:4-12)
+
+
+def _weight_array(w: np.ndarray, w_dtype: int) -> np.ndarray:
+    return _c(w, {W_F32: np.float32, W_BF16: np.uint16, W_I8: np.int8}[w_dtype])
+
+
+def matmul(x, w, w_dtype: int, scale=None, bias=None, threads: int = 8) -> np.ndarray:
+    """y = x . W^T (* row scale for I8) + bias: the reference's scalar matmul
+    (src/matrix.cpp:131-146,247-265). x: [T, cols]; w: [rows, cols] as f32, bf16 bits
+    (uint16) or int8."""
+    x = _c(x, np.float32)
+    w = _weight_array(w, w_dtype)
+    rows, cols = w.shape
+    T = x.size // cols
+    y = np.empty((T, rows), np.float32)
+    sc = None if scale is None else _c(scale, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    orc().orc_matmul(_ptr(y), _ptr(x), _ptr(w), w_dtype, None if sc is None else _ptr(sc),
+                     None if b is None else _ptr(b), T, rows, cols, threads)
+    return y
+
+
+def quantize_i8(w) -> tuple[np.ndarray, np.ndarray]:
+    """Per-row symmetric int8 quantization (src/matrix.cpp:84-97): (q [rows, cols], scale [rows])."""
+    w = _c(w, np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    orc().orc_quantize_i8(_ptr(q), _ptr(s), _ptr(w), rows, cols)
+    return q, s
+
+
+def row_to_f32(w, w_dtype: int, r: int, scale=None) -> np.ndarray:
+    """Row r widened to f32 (src/matrix.cpp:60-67)."""
+    w = _weight_array(w, w_dtype)
+    out = np.empty(w.shape[1], np.float32)
+    sc = None if scale is None else _c(scale, np.float32)
+    orc().orc_row_to_f32(_ptr(out), _ptr(w), w_dtype, None if sc is None else _ptr(sc),
+                         w.shape[1], r)
+    return out
+
+
+def rmsnorm(x, weight, eps: float) -> np.ndarray:
+    """src/ops.cpp:23-32."""
+    x = _c(x, np.float32)
+    weight = _c(weight, np.float32)
+    dim = weight.size
+    y = np.empty_like(x)
+    orc().orc_rmsnorm(_ptr(y), _ptr(x), _ptr(weight), x.size // dim, dim, ctypes.c_float(eps))
+    return y
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    """silu(gate) * up, elementwise (src/ops.cpp:68, src/model.cpp:86)."""
+    g = _c(gate, np.float32).copy()
+    u = _c(up, np.float32)
+    orc().orc_silu_mul(_ptr(g), _ptr(u), ctypes.c_size_t(g.size))
+    return g
+
+
+def ref_matmul_bf16(x, w_bits, dtype: int, bias=None, kernel: int = 0):
+    """The reference's own ie::matmul on a bf16-bits matrix stored as `dtype`
+    (0 F32, 1 BF16, 2 I8), kernel 0 scalar / 1 AVX2 (oracle/_ref). Returns
+    (y, i8 scales or None, i8 values or None)."""
+    x = _c(x, np.float32)
+    w = _c(w_bits, np.uint16)
+    rows, cols = w.shape
+    T = x.size // cols
+    y = np.empty((T, rows), np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    sc = np.empty(rows, np.float32) if dtype == W_I8 else None
+    q = np.empty((rows, cols), np.int8) if dtype == W_I8 else None
+    ref().ref_matmul_bf16(_ptr(y), _ptr(x), _ptr(w), dtype, None if b is None else _ptr(b), T,
+                          rows, cols, kernel, None if sc is None else _ptr(sc),
+                          None if q is None else _ptr(q))
+    return y, sc, q
+
+
+def ref_rmsnorm(x, weight, eps: float) -> np.ndarray:
+    x = _c(x, np.float32)
+    weight = _c(weight, np.float32)
+    y = np.empty_like(x)
+    ref().ref_rmsnorm(_ptr(y), _ptr(x), _ptr(weight), x.size // weight.size, weight.size,
+                      ctypes.c_float(eps))
+    return y
+
+
+def ref_silu(x: float) -> float:
+    f = ref().ref_silu
+    f.restype, f.argtypes = ctypes.c_float, [ctypes.c_float]
+    return float(f(x))
+
+
+def ref_row_to_f32(w_bits, dtype: int, r: int) -> np.ndarray:
+    w = _c(w_bits, np.uint16)
+    out = np.empty(w.shape[1], np.float32)
+    ref().ref_row_to_f32(_ptr(out), _ptr(w), dtype, w.shape[0], w.shape[1], r)
+    return out

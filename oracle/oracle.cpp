@@ -398,6 +398,78 @@ void orc_gather_rows(float* dst, const float* src, const int32_t* rows, int R, i
     std::memcpy(dst + size_t(r) * dim, src + size_t(rows[r]) * dim, size_t(dim) * sizeof(float));
 }
 
+namespace {
+
+float weight_at(const void* w, int w_dtype, size_t i) {
+  if (w_dtype == ORC_W_F32) return static_cast<const float*>(w)[i];
+  if (w_dtype == ORC_W_BF16) return orc_bf16_to_f32(static_cast<const uint16_t*>(w)[i]);
+  return float(static_cast<const int8_t*>(w)[i]);
+}
+
+}  // namespace
+
+void orc_matmul(float* y, const float* x, const void* w, int w_dtype, const float* scale,
+                const float* bias, int T, int rows, int cols, int threads) {
+  auto body = [&](int64_t r0, int64_t r1) {
+    for (int64_t o = r0; o < r1; ++o) {
+      const size_t base = size_t(o) * cols;
+      const float s = w_dtype == ORC_W_I8 ? scale[o] : 1.0f;
+      const float b = bias ? bias[o] : 0.0f;
+      for (int t = 0; t < T; ++t) {
+        const float* xt = x + size_t(t) * cols;
+        float acc = 0.0f;
+        if (w_dtype == ORC_W_F32) {  // compiled without contraction there
+          for (int k = 0; k < cols; ++k) acc += weight_at(w, w_dtype, base + k) * xt[k];
+        } else {
+          for (int k = 0; k < cols; ++k) acc = std::fma(weight_at(w, w_dtype, base + k), xt[k], acc);
+        }
+        y[size_t(t) * rows + o] = acc * s + b;
+      }
+    }
+  };
+  pool_with(threads).run(rows, body);
+}
+
+void orc_quantize_i8(int8_t* q, float* scale, const float* w, int rows, int cols) {
+  for (int r = 0; r < rows; ++r) {
+    const float* row = w + size_t(r) * cols;
+    float amax = 0.0f;
+    for (int i = 0; i < cols; ++i) amax = std::max(amax, std::fabs(row[i]));
+    const float s = amax > 0 ? amax / 127.0f : 1.0f;
+    scale[r] = s;
+    for (int i = 0; i < cols; ++i) {
+      const float v = std::nearbyint(row[i] / s);
+      q[size_t(r) * cols + i] = int8_t(std::max(-127.0f, std::min(127.0f, v)));
+    }
+  }
+}
+
+void orc_row_to_f32(float* out, const void* w, int w_dtype, const float* scale, int cols, int r) {
+  const size_t base = size_t(r) * cols;
+  for (int i = 0; i < cols; ++i) {
+    const float v = weight_at(w, w_dtype, base + i);
+    out[i] = w_dtype == ORC_W_I8 ? scale[r] * v : v;
+  }
+}
+
+void orc_rmsnorm(float* y, const float* x, const float* weight, int T, int dim, float eps) {
+  for (int t = 0; t < T; ++t) {
+    const float* xt = x + size_t(t) * dim;
+    float* yt = y + size_t(t) * dim;
+    float sum_sq = 0.0f;
+    for (int i = 0; i < dim; ++i) sum_sq += xt[i] * xt[i];  // not contracted there
+    const float inv_rms = 1.0f / std::sqrt(sum_sq / float(dim) + eps);
+    for (int i = 0; i < dim; ++i) yt[i] = xt[i] * inv_rms * weight[i];
+  }
+}
+
+void orc_silu_mul(float* gate, const float* up, size_t n) {
+  for (size_t i = 0; i < n; ++i) {
+    const float g = gate[i];
+    gate[i] = g / (1.0f + std::exp(-g)) * up[i];
+  }
+}
+
 double orc_compare(const float* got, const float* want, size_t n, double* max_abs_err,
                    size_t* worst_index) {
   double max_err = 0, max_ref = 0;

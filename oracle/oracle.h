@@ -28,6 +28,11 @@
 //   orc_rope_append_paged, orc_paged_attention   composition of the above;
 //       golden fixtures under tests/golden/ made from oracle/_ref.
 //   orc_compare                                numpy restatement of the metric.
+//   orc_matmul, orc_quantize_i8, orc_row_to_f32   bit-exact vs the reference's
+//       own ie::matmul (scalar kernel) and ie::make_matrix / row_to_f32
+//       (oracle/_ref); identity and one-hot matrices; fp64 dot products.
+//   orc_rmsnorm, orc_silu_mul                   bit-exact vs ie::rmsnorm /
+//       ie::silu (oracle/_ref); closed forms (constant rows, silu(0) = 0).
 #pragma once
 
 #include <stddef.h>
@@ -110,6 +115,38 @@ void orc_paged_attention(float* out, const float* q, const void* k_pool, const v
 
 // dst[r, :] = src[rows[r], :]. Reference: src/cuda/kernels.cu:778-783.
 void orc_gather_rows(float* dst, const float* src, const int32_t* rows, int R, int dim);
+
+// ------------------------------------------------ the decode step's layer ---
+// Weight formats of the reference's Matrix (src/matrix.h:4-12): F32, BF16 bits,
+// or I8 with one f32 scale per row. Same codes as include/ie_hip.h.
+enum { ORC_W_F32 = 0, ORC_W_BF16 = 1, ORC_W_I8 = 2 };
+
+// y[t][o] = (sum_k w[o][k] * x[t][k]) * s[o] + bias[o] (s = scale[o] for I8,
+// else 1; bias may be null), the reference's scalar kernel and row loop
+// (src/matrix.cpp:131-146,247-265): per token, the products summed in k order
+// from 0 (one fma each for BF16 and I8 weights, as GCC compiles those
+// instantiations; a multiply and an add for F32), the scale and then the bias
+// applied after the sum. x: [T, cols], y: [T, rows]. Rows are split over
+// `threads`.
+void orc_matmul(float* y, const float* x, const void* w, int w_dtype, const float* scale,
+                const float* bias, int T, int rows, int cols, int threads);
+
+// Symmetric per-row int8 quantization, as ie::make_matrix builds an I8 matrix
+// (src/matrix.cpp:84-97): s = max|w| / 127 (1 for an all-zero row), q =
+// clamp(nearbyint(w / s), -127, 127).
+void orc_quantize_i8(int8_t* q, float* scale, const float* w, int rows, int cols);
+
+// One row of a weight matrix widened to f32 (ie::Matrix::row_to_f32,
+// src/matrix.cpp:60-67): the embedding lookup of src/model.cpp:53-56.
+void orc_row_to_f32(float* out, const void* w, int w_dtype, const float* scale, int cols, int r);
+
+// ie::rmsnorm (src/ops.cpp:23-32): sum of squares in order (a multiply and an
+// add each, as compiled there), then y = x * (1 / sqrt(sum / dim + eps)) * weight.
+void orc_rmsnorm(float* y, const float* x, const float* weight, int T, int dim, float eps);
+
+// gate[i] = silu(gate[i]) * up[i], silu(x) = x / (1 + exp(-x)) (src/ops.cpp:68,
+// src/model.cpp:86).
+void orc_silu_mul(float* gate, const float* up, size_t n);
 
 // max|got - want| / max|want| (NaN counts as the worst error).
 // Reference: src/npy.cpp:98-110.
