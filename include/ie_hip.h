@@ -183,6 +183,48 @@ int ie_hip_gather_rows(float* dst, const float* src, const int32_t* rows, int R,
 int ie_hip_gather_kv(float* dst, const void* pool, ie_kv_layout kv, int seq, int len, int kv_dim,
                      hipStream_t stream);
 
+/* -------------------------------------------- the decode step's dense ops ---
+ * The ops around the paged path in the reference's per-layer enqueue
+ * (src/cuda/cuda_runner.cu:427-458): embedding, rmsnorm, the q/k/v, o_proj
+ * and down projections, and the fused gate/up + SiLU. Activations are f32.
+ * Results agree with the reference CPU path (src/ops.cpp, src/matrix.cpp)
+ * to float32 rounding of the sums (max |d| / max |ref| <= 1e-5); the
+ * embedding is exact. */
+
+/* A weight matrix in device memory, [rows, cols] row-major: BF16 bits, or
+ * INT8 values with one f32 scale per row (`scale`, INT8 only). Replaces
+ * DeviceMatrix (src/cuda/kernels.cuh:40-46). */
+typedef struct ie_matrix {
+  const void* data;
+  const float* scale;
+  int32_t int8;
+  int32_t rows, cols;
+} ie_matrix;
+
+/* x[t, :] = E[ids[t], :] widened to f32 (times the row's scale for INT8).
+ * Replaces embedding (src/cuda/kernels.cuh:48-49, kernels.cu:191-198). */
+int ie_hip_embedding(float* x, const int32_t* ids, ie_matrix e, int T, hipStream_t stream);
+
+/* y[t, :] = x[t, :] * (1 / sqrt(mean(x[t, :]^2) + eps)) * weight; y may equal
+ * x. Replaces rmsnorm (src/cuda/kernels.cuh:51-53, kernels.cu:200-209). */
+int ie_hip_rmsnorm(float* y, const float* x, const float* weight, int T, int dim, float eps,
+                   hipStream_t stream);
+
+/* y[t, o] (+)= (sum_k W[o, k] * x[t, k]) * scale[o] + bias[o] (scale: INT8
+ * only; bias may be NULL). accumulate != 0 adds into y (the residual
+ * connection). x: [T, w.cols], y: [T, w.rows]; w.cols a multiple of 8; x and
+ * the weights 16-byte aligned (8 for INT8). Replaces matmul
+ * (src/cuda/kernels.cuh:55-62, kernels.cu:211-241,1242-1253). */
+int ie_hip_matmul(float* y, const float* x, ie_matrix w, const float* bias, int T, int accumulate,
+                  hipStream_t stream);
+
+/* out[t, o] = silu(x[t] . Wg[o] * sg[o]) * (x[t] . Wu[o] * su[o]), silu(v) =
+ * v / (1 + exp(-v)): the MLP's gate and up projections and the SwiGLU in one
+ * launch. Wg and Wu of the same shape and format. Replaces gate_up_silu
+ * (src/cuda/kernels.cuh:64-66). */
+int ie_hip_gate_up_silu(float* out, const float* x, ie_matrix w_gate, ie_matrix w_up, int T,
+                        hipStream_t stream);
+
 /* ------------------------------------------------------- page allocator ---
  * The page pool / free list / page tables behind BatchRunner (reference:
  * CudaEngine ctor src/cuda/cuda_runner.cu:191-204, open/close_sequence

@@ -43,6 +43,14 @@ class KvLayout(ctypes.Structure):
                 ("num_pages", ctypes.c_int32)]
 
 
+class Matrix(ctypes.Structure):
+    """ie_matrix: the reference's DeviceMatrix (src/cuda/kernels.cuh:40-46), BF16 bits or
+    INT8 values with one f32 scale per row."""
+
+    _fields_ = [("data", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("int8", ctypes.c_int32),
+                ("rows", ctypes.c_int32), ("cols", ctypes.c_int32)]
+
+
 _vp, _i, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
 _SIGS = {
     "ie_hip_last_error": (ctypes.c_char_p, []),
@@ -63,6 +71,10 @@ _SIGS = {
     "ie_hip_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _i, _vp]),
     "ie_hip_gather_rows": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "ie_hip_gather_kv": (_i, [_vp, _vp, KvLayout, _i, _i, _i, _vp]),
+    "ie_hip_embedding": (_i, [_vp, _vp, Matrix, _i, _vp]),
+    "ie_hip_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "ie_hip_matmul": (_i, [_vp, _vp, Matrix, _vp, _i, _i, _vp]),
+    "ie_hip_gate_up_silu": (_i, [_vp, _vp, Matrix, Matrix, _i, _vp]),
     "ie_pages_create": (_vp, [_i, _i, _i]),
     "ie_pages_destroy": (None, [_vp]),
     "ie_pages_open_sequence": (_i, [_vp]),
@@ -230,6 +242,41 @@ def gather_rows(dst, src, rows, stream=None) -> None:
     """dst[r] = src[rows[r]] (src/cuda/kernels.cuh:101-102)."""
     _check(lib().ie_hip_gather_rows(_ptr(dst), _ptr(src), _ptr(rows), rows.numel(), src.shape[-1],
                                     _stream(stream)))
+
+
+def matrix(data, scale=None) -> Matrix:
+    """An ie_matrix over a device tensor of BF16 bits (int16/uint16/bfloat16) or INT8
+    values [rows, cols] and, for INT8, its f32 row scales."""
+    import torch
+    int8 = data.dtype == torch.int8
+    if int8 and scale is None:
+        raise ValueError("INT8 weights need their row scales")
+    return Matrix(data.data_ptr(), scale.data_ptr() if int8 else None, int(int8), data.shape[0],
+                  data.shape[1])
+
+
+def embedding(x, ids, e: Matrix, stream=None) -> None:
+    """x[t] = E[ids[t]] widened to f32 (src/cuda/kernels.cuh:48-49)."""
+    _check(lib().ie_hip_embedding(_ptr(x), _ptr(ids), e, ids.numel(), _stream(stream)))
+
+
+def rmsnorm(y, x, weight, eps: float, stream=None) -> None:
+    """y = x / rms(x) * weight per row (src/cuda/kernels.cuh:51-53)."""
+    dim = weight.numel()
+    _check(lib().ie_hip_rmsnorm(_ptr(y), _ptr(x), _ptr(weight), x.numel() // dim, dim, eps,
+                                _stream(stream)))
+
+
+def matmul(y, x, w: Matrix, bias=None, accumulate: bool = False, stream=None) -> None:
+    """y (+)= x . W^T * scale + bias (src/cuda/kernels.cuh:55-62)."""
+    _check(lib().ie_hip_matmul(_ptr(y), _ptr(x), w, _ptr(bias), x.numel() // w.cols,
+                               int(accumulate), _stream(stream)))
+
+
+def gate_up_silu(out, x, w_gate: Matrix, w_up: Matrix, stream=None) -> None:
+    """out = silu(x . Wg^T) * (x . Wu^T) (src/cuda/kernels.cuh:64-66)."""
+    _check(lib().ie_hip_gate_up_silu(_ptr(out), _ptr(x), w_gate, w_up, x.numel() // w_gate.cols,
+                                     _stream(stream)))
 
 
 def gather_kv(dst, pool, tables, max_pages: int, seq: int, length: int, kv_dim: int,

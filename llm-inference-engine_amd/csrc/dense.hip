@@ -1,0 +1,239 @@
+// The dense ops of the decode step around the paged-KV path (gfx950): the
+// embedding lookup, rmsnorm, the projections (q/k/v, o_proj, down) and the
+// fused gate/up + SiLU. Reference: src/cuda/kernels.cuh:40-66 and
+// src/cuda/kernels.cu:191-241,1236-1285; CPU semantics src/ops.cpp:23-32,68,
+// src/matrix.cpp:131-146,247-289, src/model.cpp:53-90.
+//
+// Weights are BF16 bits or INT8 with one f32 scale per row (the reference's
+// DeviceMatrix). Activations are f32.
+//
+// matmul_mfma_kernel: y[t][o] (+)= (sum_k W[o][k] x[t][k]) * s[o] + bias[o] on
+// v_mfma_f32_16x16x32_bf16. A workgroup owns a 16-row x 16-token output tile:
+//   D[16 rows x 16 tokens] = W[16 x K] . x^T[K x 16]
+// The weights enter the MFMA exactly (BF16 as stored; INT8 values widened to
+// bf16, exact for |q| <= 127). Each activation is split into three bf16
+// parts, x = hi + mid + lo exactly (each remainder is exact in f32 and holds
+// at most 16, then 8, significant bits), and each block is multiplied three
+// times, so every product is the f32-exact w * x. Only the summation order
+// differs from the CPU's: the results agree to float32 rounding of the sum.
+// The 4 waves of a workgroup take interleaved 32-wide K blocks and their
+// partial tiles are added through LDS in wave order, so results do not depend
+// on scheduling. At decode batch sizes this gives rows/16 x T/16 workgroups
+// (224 for 896 rows and 64 tokens, 1,216 for the 4,864-row gate/up).
+// Lane (g, r) of a tile: A = W[row r][k + 8g .. +8], B = x[token r][k + 8g ..
+// +8]; the result lane holds rows 4g .. 4g+3 of token r.
+#include "common.hpp"
+#include "mfma.hpp"
+
+namespace iehip {
+namespace {
+
+constexpr int kMmWaves = 4;  // K split of a 16 x 16 output tile
+
+using bf16 = __bf16;
+
+__device__ __forceinline__ bf16x8 load_weights(const void* w, bool int8, size_t idx) {
+  bf16x8 a;
+  if (!int8) {
+    a = *reinterpret_cast<const bf16x8*>(static_cast<const uint16_t*>(w) + idx);
+  } else {
+    const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(w) + idx);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t word = j < 4 ? raw.x : raw.y;
+      const int8_t q = static_cast<int8_t>((word >> (8 * (j & 3))) & 0xFF);
+      a[j] = static_cast<bf16>(static_cast<float>(q));
+    }
+  }
+  return a;
+}
+
+// 8 activations as three bf16 operands whose sum is exact.
+__device__ __forceinline__ void split3(const float4 p, const float4 q, bf16x8& hi, bf16x8& mid,
+                                       bf16x8& lo) {
+  const float v[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bf16 h = static_cast<bf16>(v[j]);
+    const float r1 = v[j] - static_cast<float>(h);
+    const bf16 m = static_cast<bf16>(r1);
+    const float r2 = r1 - static_cast<float>(m);
+    hi[j] = h;
+    mid[j] = m;
+    lo[j] = static_cast<bf16>(r2);
+  }
+}
+
+__device__ __forceinline__ f32x4 mma3(bf16x8 a, bf16x8 bh, bf16x8 bm, bf16x8 bl, f32x4 c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bm, c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// GATE: out = silu(x . Wg^T * sg) * (x . Wu^T * su) (gate_up_silu); otherwise
+// y (+)= x . W^T * s + bias. cols % 8 == 0; the K tail past cols is zero.
+template <bool GATE>
+__global__ void __launch_bounds__(64 * kMmWaves)
+matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const void* __restrict__ w,
+                   const float* __restrict__ scale, const void* __restrict__ w2,
+                   const float* __restrict__ scale2, const float* __restrict__ bias, int int8,
+                   int T, int rows, int cols, int accumulate) {
+  __shared__ f32x4 red[GATE ? 2 : 1][kMmWaves - 1][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int row0 = blockIdx.x * 16, tok0 = blockIdx.y * 16;
+  const size_t wrow = size_t(min(row0 + r, rows - 1)) * cols;     // rows past the end: last row
+  const float* xrow = x + size_t(min(tok0 + r, T - 1)) * cols;   // tokens likewise
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = acc;
+  for (int kb = 32 * wave; kb < cols; kb += 32 * kMmWaves) {
+    const int k = kb + 8 * g;
+    bf16x8 a = {}, a2 = {}, bh = {}, bm = {}, bl = {};
+    if (k < cols) {
+      a = load_weights(w, int8, wrow + k);
+      if constexpr (GATE) a2 = load_weights(w2, int8, wrow + k);
+      const float4* xp = reinterpret_cast<const float4*>(xrow + k);
+      split3(xp[0], xp[1], bh, bm, bl);
+    }
+    acc = mma3(a, bh, bm, bl, acc);
+    if constexpr (GATE) acc2 = mma3(a2, bh, bm, bl, acc2);
+  }
+  // Partial tiles of waves 1..3 through LDS, added to wave 0's in wave order.
+  if (wave > 0) {
+    red[0][wave - 1][lane] = acc;
+    if constexpr (GATE) red[GATE ? 1 : 0][wave - 1][lane] = acc2;
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int v = 0; v < kMmWaves - 1; ++v) {
+    acc += red[0][v][lane];
+    if constexpr (GATE) acc2 += red[GATE ? 1 : 0][v][lane];
+  }
+  const int tok = tok0 + r;
+  if (tok >= T) return;
+  float* yt = y + size_t(tok) * rows;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + 4 * g + i;
+    if (row >= rows) break;
+    float v = acc[i] * (int8 ? scale[row] : 1.0f);
+    if constexpr (GATE) {
+      v = silu(v) * (acc2[i] * (int8 ? scale2[row] : 1.0f));
+    } else {
+      if (bias) v += bias[row];
+      if (accumulate) v += yt[row];
+    }
+    yt[row] = v;
+  }
+}
+
+// y[t] = x[t] * (1 / sqrt(mean(x[t]^2) + eps)) * weight; one workgroup per row.
+// Each element is read and written by the same thread, so y may equal x.
+__global__ void __launch_bounds__(256)
+rmsnorm_kernel(float* y, const float* x, const float* __restrict__ weight, int dim, float eps) {
+  __shared__ float part[4];
+  const float* xt = x + size_t(blockIdx.x) * dim;
+  float* yt = y + size_t(blockIdx.x) * dim;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += xt[i] * xt[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float inv_rms = 1.0f / sqrtf(total / float(dim) + eps);
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) yt[i] = xt[i] * inv_rms * weight[i];
+}
+
+// x[t] = E[ids[t]] widened to f32 (times the row's scale for INT8).
+__global__ void __launch_bounds__(256)
+embedding_kernel(float* __restrict__ x, const int32_t* __restrict__ ids, const void* __restrict__ e,
+                 const float* __restrict__ scale, int int8, int dim) {
+  const int id = ids[blockIdx.x];
+  float* xt = x + size_t(blockIdx.x) * dim;
+  if (int8) {
+    const int8_t* row = static_cast<const int8_t*>(e) + size_t(id) * dim;
+    const float s = scale[id];
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) xt[i] = s * static_cast<float>(row[i]);
+  } else {
+    const uint16_t* row = static_cast<const uint16_t*>(e) + size_t(id) * dim;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x)
+      xt[i] = __uint_as_float(static_cast<uint32_t>(row[i]) << 16);
+  }
+}
+
+int check_matrix(const ie_matrix& m, const char* who) {
+  if (!m.data || m.rows <= 0 || m.cols <= 0)
+    return fail(IE_HIP_EINVAL, std::string(who) + ": empty weight matrix");
+  if (m.int8 && !m.scale) return fail(IE_HIP_EINVAL, std::string(who) + ": INT8 needs row scales");
+  return IE_HIP_OK;
+}
+
+int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const ie_matrix* w2,
+                  const float* bias, int T, int accumulate, hipStream_t stream, const char* who) {
+  if (int rc = check_matrix(w, who)) return rc;
+  if (w2) {
+    if (int rc = check_matrix(*w2, who)) return rc;
+    if (w2->rows != w.rows || w2->cols != w.cols || w2->int8 != w.int8)
+      return fail(IE_HIP_EINVAL, std::string(who) + ": gate and up shapes differ");
+  }
+  if (T < 0) return fail(IE_HIP_EINVAL, std::string(who) + ": T < 0");
+  if (T == 0) return IE_HIP_OK;
+  if (!y || !x) return fail(IE_HIP_EINVAL, std::string(who) + ": null pointer");
+  if (w.cols % 8)
+    return fail(IE_HIP_EINVAL, std::string(who) + ": cols must be a multiple of 8");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w.data) |
+                          (w2 ? reinterpret_cast<uintptr_t>(w2->data) : 0);
+  if (align & (w.int8 ? 7 : 15))
+    return fail(IE_HIP_EINVAL, std::string(who) + ": x and the weights must be 16-byte aligned");
+  const dim3 grid((w.rows + 15) / 16, (T + 15) / 16), block(64 * kMmWaves);
+  if (grid.y > 65535) return fail(IE_HIP_EINVAL, std::string(who) + ": too many tokens");
+  if (gate)
+    hipLaunchKernelGGL(matmul_mfma_kernel<true>, grid, block, 0, stream, y, x, w.data, w.scale,
+                       w2->data, w2->scale, nullptr, w.int8, T, w.rows, w.cols, 0);
+  else
+    hipLaunchKernelGGL(matmul_mfma_kernel<false>, grid, block, 0, stream, y, x, w.data, w.scale,
+                       nullptr, nullptr, bias, w.int8, T, w.rows, w.cols, accumulate);
+  return check_launch(who);
+}
+
+}  // namespace
+}  // namespace iehip
+
+using namespace iehip;
+
+extern "C" int ie_hip_embedding(float* x, const int32_t* ids, ie_matrix e, int T,
+                                hipStream_t stream) {
+  clear_error();
+  if (int rc = check_matrix(e, "embedding")) return rc;
+  if (T < 0) return fail(IE_HIP_EINVAL, "embedding: T < 0");
+  if (T == 0) return IE_HIP_OK;
+  if (!x || !ids) return fail(IE_HIP_EINVAL, "embedding: null pointer");
+  hipLaunchKernelGGL(embedding_kernel, dim3(T), dim3(256), 0, stream, x, ids, e.data, e.scale,
+                     e.int8, e.cols);
+  return check_launch("embedding");
+}
+
+extern "C" int ie_hip_rmsnorm(float* y, const float* x, const float* weight, int T, int dim,
+                              float eps, hipStream_t stream) {
+  clear_error();
+  if (T < 0 || dim <= 0) return fail(IE_HIP_EINVAL, "rmsnorm: bad sizes");
+  if (T == 0) return IE_HIP_OK;
+  if (!y || !x || !weight) return fail(IE_HIP_EINVAL, "rmsnorm: null pointer");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, stream, y, x, weight, dim, eps);
+  return check_launch("rmsnorm");
+}
+
+extern "C" int ie_hip_matmul(float* y, const float* x, ie_matrix w, const float* bias, int T,
+                             int accumulate, hipStream_t stream) {
+  clear_error();
+  return launch_matmul(false, y, x, w, nullptr, bias, T, accumulate, stream, "matmul");
+}
+
+extern "C" int ie_hip_gate_up_silu(float* out, const float* x, ie_matrix w_gate, ie_matrix w_up,
+                                   int T, hipStream_t stream) {
+  clear_error();
+  return launch_matmul(true, out, x, w_gate, &w_up, nullptr, T, 0, stream, "gate_up_silu");
+}

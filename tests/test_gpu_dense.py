@@ -1,0 +1,134 @@
+"""The decode step's dense ops on the GPU vs the CPU oracle (itself bit-exact with the
+reference's src/matrix.cpp and src/ops.cpp): embedding (exact), rmsnorm, matmul with BF16
+and INT8 weights (bias, residual accumulation, ragged shapes), the fused gate/up + SiLU.
+
+Tolerance: the fp32 bar of the north star, max |d| / max |ref| <= 1e-5 (the reference's
+metric, src/npy.cpp:98-110). Only summation order differs: the MFMA kernel multiplies the
+weights (exact in bf16) by each activation split into three bf16 parts, which is the exact
+f32 product."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+REL = 1e-5
+
+
+def rel_err(got, want):
+    return O.compare(got, want)[0]
+
+
+def bf16_bits(x):
+    return O.round_to_kv(np.asarray(x, np.float32), 2)
+
+
+def widen(bits):
+    return O.widen_kv(bits, 2).reshape(bits.shape)
+
+
+def dev_weights(ie, dev, w32, int8):
+    """(ie_matrix, keep-alive tensors, oracle args) for f32 master weights."""
+    if int8:
+        q, s = O.quantize_i8(w32)
+        dq = torch.from_numpy(q).to(dev)
+        ds = torch.from_numpy(s).to(dev)
+        return ie.matrix(dq, ds), (dq, ds), (q, O.W_I8, s)
+    b = bf16_bits(w32)
+    db = torch.from_numpy(b.view(np.int16)).to(dev)
+    return ie.matrix(db), (db,), (b, O.W_BF16, None)
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_embedding_exact(ie, dev, int8):
+    rng = np.random.default_rng(1)
+    vocab, dim = 1000, 896
+    table = rng.standard_normal((vocab, dim), dtype=np.float32)
+    m, keep, (w, fmt, s) = dev_weights(ie, dev, table, int8)
+    ids = np.array([0, vocab - 1, 5, 5, 731, 2], np.int32)
+    x = torch.full((ids.size, dim), float("nan"), device=dev)
+    ie.embedding(x, torch.from_numpy(ids).to(dev), m)
+    torch.cuda.synchronize()
+    got = x.cpu().numpy()
+    want = np.stack([O.row_to_f32(w, fmt, int(i), s) for i in ids])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dim", [64, 896, 4864])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_rmsnorm(ie, dev, dim, in_place):
+    rng = np.random.default_rng(dim)
+    x = rng.standard_normal((33, dim), dtype=np.float32) * np.float32(4.0)
+    w = rng.standard_normal(dim, dtype=np.float32)
+    dx = torch.from_numpy(x).to(dev)
+    y = dx if in_place else torch.empty_like(dx)
+    ie.rmsnorm(y, dx, torch.from_numpy(w).to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu().numpy(), O.rmsnorm(x, w, 1e-6)) <= REL
+
+
+MATMULS = [
+    # T, rows, cols, bias, accumulate
+    (1, 896, 896, True, False),      # q_proj, one token
+    (64, 128, 896, True, False),     # k/v_proj at decode batch 64
+    (64, 896, 896, False, True),     # o_proj into the residual
+    (64, 896, 4864, False, True),    # down_proj into the residual
+    (37, 130, 104, True, True),      # ragged: rows % 16, cols % 32, T % 16 all nonzero
+    (300, 896, 896, True, False),    # a prompt chunk
+]
+
+
+@pytest.mark.parametrize("case", range(len(MATMULS)))
+@pytest.mark.parametrize("int8", [False, True])
+def test_matmul(ie, dev, case, int8):
+    T, rows, cols, with_bias, acc = MATMULS[case]
+    rng = np.random.default_rng(100 + case)
+    x = rng.standard_normal((T, cols), dtype=np.float32)
+    w32 = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+    bias = rng.standard_normal(rows, dtype=np.float32) if with_bias else None
+    y0 = rng.standard_normal((T, rows), dtype=np.float32)
+    m, keep, (w, fmt, s) = dev_weights(ie, dev, w32, int8)
+    y = torch.from_numpy(y0).to(dev)
+    ie.matmul(y, torch.from_numpy(x).to(dev), m,
+              None if bias is None else torch.from_numpy(bias).to(dev), accumulate=acc)
+    torch.cuda.synchronize()
+    want = O.matmul(x, w, fmt, s, bias)
+    if acc:
+        want = want + y0  # the CPU adds the projection into x afterwards (src/model.cpp:80)
+    assert rel_err(y.cpu().numpy(), want) <= REL
+
+
+@pytest.mark.parametrize("int8", [False, True])
+@pytest.mark.parametrize("T", [1, 64])
+def test_gate_up_silu(ie, dev, int8, T):
+    rng = np.random.default_rng(7 + T)
+    rows, cols = 4864, 896
+    x = rng.standard_normal((T, cols), dtype=np.float32)
+    wg32 = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+    wu32 = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+    mg, kg, (wg, fmt, sg) = dev_weights(ie, dev, wg32, int8)
+    mu, ku, (wu, _, su) = dev_weights(ie, dev, wu32, int8)
+    out = torch.full((T, rows), float("nan"), device=dev)
+    ie.gate_up_silu(out, torch.from_numpy(x).to(dev), mg, mu)
+    torch.cuda.synchronize()
+    want = O.silu_mul(O.matmul(x, wg, fmt, sg), O.matmul(x, wu, fmt, su))
+    assert rel_err(out.cpu().numpy(), want) <= REL
+
+
+def test_dense_argument_errors(ie, dev):
+    x = torch.zeros((4, 12), device=dev)
+    y = torch.zeros((4, 16), device=dev)
+    w = torch.zeros((16, 12), dtype=torch.int16, device=dev)
+    with pytest.raises(ie.IeHipError, match="multiple of 8"):
+        ie.matmul(y, x, ie.matrix(w))
+    q = torch.zeros((16, 16), dtype=torch.int8, device=dev)
+    bad = ie.Matrix(q.data_ptr(), None, 1, 16, 16)
+    with pytest.raises(ie.IeHipError, match="scales"):
+        ie.matmul(y, torch.zeros((4, 16), device=dev), bad)
+    w1 = torch.zeros((16, 16), dtype=torch.int16, device=dev)
+    w2 = torch.zeros((8, 16), dtype=torch.int16, device=dev)
+    with pytest.raises(ie.IeHipError, match="shapes differ"):
+        ie.gate_up_silu(y, torch.zeros((4, 16), device=dev), ie.matrix(w1), ie.matrix(w2))
