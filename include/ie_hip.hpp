@@ -101,6 +101,24 @@ inline size_t attention_workspace_bytes(int T, int n_heads, int head_dim, int nu
   return ie_hip_attention_workspace_bytes(T, n_heads, head_dim, num_chunks);
 }
 
+/* embedding / rmsnorm / matmul / gate_up_silu (kernels.cuh:48-66) over an
+ * ie_matrix (DeviceMatrix, kernels.cuh:40-46). */
+inline void embedding(float* x, const int32_t* ids, const ie_matrix& e, int T, hipStream_t stream) {
+  check(ie_hip_embedding(x, ids, e, T, stream));
+}
+inline void rmsnorm(float* y, const float* x, const float* weight, int T, int dim, float eps,
+                    hipStream_t stream) {
+  check(ie_hip_rmsnorm(y, x, weight, T, dim, eps, stream));
+}
+inline void matmul(float* y, const float* x, const ie_matrix& w, const float* bias, int T,
+                   bool accumulate, hipStream_t stream) {
+  check(ie_hip_matmul(y, x, w, bias, T, accumulate ? 1 : 0, stream));
+}
+inline void gate_up_silu(float* out, const float* x, const ie_matrix& wg, const ie_matrix& wu,
+                         int T, hipStream_t stream) {
+  check(ie_hip_gate_up_silu(out, x, wg, wu, T, stream));
+}
+
 /* gather_rows (kernels.cuh:101-102). */
 inline void gather_rows(float* dst, const float* src, const int* rows, int R, int dim,
                         hipStream_t stream) {

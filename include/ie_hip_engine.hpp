@@ -241,6 +241,12 @@ class KvEngine {
 
   const StepInfo& last_step() const { return last_; }
   int decode_graphs() const { return int(graphs_.size()); }
+  /* Replaces the model's per-layer work (for a body that needs the engine
+   * itself, as DecoderModel's does); recorded decode graphs are dropped. */
+  void set_body(LayerBody body) {
+    body_ = std::move(body);
+    drop_graphs();
+  }
   int max_pages_per_seq() const { return max_pages_per_seq_; }
   const int32_t* host_tables() const { return ie_pages_host_tables(pages_); }
   const int32_t* device_tables() const { return tables_; }

@@ -40,3 +40,25 @@ def test_engine_selftest(kv):
     fails = [l for l in r.stdout.splitlines() if l.startswith("FAIL")]
     assert r.returncode == 0 and not fails, "\n".join(fails) or f"exit status {r.returncode}"
     assert " checks, 0 failures" in r.stdout
+
+
+MODEL_BIN = os.path.join(ROOT, "tests", "engine", "_bin", "model_selftest")
+
+
+def test_model_driver_built_and_linked():
+    """CPU: the decode-step driver (tests/engine/model_selftest.cpp) exists and links."""
+    assert os.path.exists(MODEL_BIN), "model_selftest not built: run __graft_entry__.build()"
+    out = subprocess.run(["ldd", MODEL_BIN], capture_output=True, text=True, check=True).stdout
+    assert "not found" not in out, out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_model_selftest(kv):
+    """A 2-layer Qwen2 decoder (Qwen2.5-0.5B layer shape) through KvEngine + DecoderModel
+    (include/ie_hip_model.hpp): prompts, decode graphs and a replay; after every step the
+    residual stream and logits against the reference's CPU forward restated on the oracle."""
+    print(f"model_selftest {kv}", flush=True)
+    r = subprocess.run([MODEL_BIN, kv], capture_output=True, text=True, timeout=110)
+    print(r.stdout[-6000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and " checks, 0 failures" in r.stdout
