@@ -26,6 +26,7 @@ Other configs print the same JSON shape for the tables in DESIGN.md:
   --config 2  RoPE + paged append, 64 rows (+ --sweep: rows per launch up to 131,072)
   --config 4  long-context decode, 24 layers, batch 1, 32k context, bf16
   --config 5  mixed step: 48 decode rows + a 4,000-token prefill (MFMA), f16
+  --config 6  the whole decode step: 24-layer Qwen2.5-0.5B-shaped decoder, batch 64, f16
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 """
 from __future__ import annotations
@@ -619,12 +620,114 @@ def copy_probe(torch, n_bytes=2 << 30):
     return round(2 * n_bytes / (ms * 1e-3) / 1e9, 1)
 
 
+def bench_model(args, torch, ie, O):
+    """Config 6: the whole decode step around the path -- a 24-layer Qwen2.5-0.5B decoder
+    (hidden 896, intermediate 4,864, 14/2 heads, tied LM head over 151,936 tokens) with
+    random BF16 weights, one new token for each of config 3's 64 rows (L ~ U[128, 4096],
+    f16 KV, shuffled 16-token pages, one pool pair per layer). Per layer: rmsnorm,
+    q/k/v, RoPE + paged append + attention (one launch), o_proj into the residual,
+    rmsnorm, gate/up + SiLU, down into the residual; then the final norm and the logits
+    of every row (src/cuda/cuda_runner.cu:418-470)."""
+    dev = torch.device("cuda:0")
+    kv = args.kv or "f16"
+    rng = np.random.default_rng(args.seed)
+    layers, B, H, I, V = 24, 64, 896, 4864, 151936
+    lens = rng.integers(128, 4097, B)
+    max_pages = 4096 // PAGE
+    num_pages = 2 * int(sum((int(n) + PAGE - 1) // PAGE for n in lens))
+    tabs = [torch.from_numpy(make_tables(rng, lens, num_pages, max_pages)).to(dev)
+            for _ in range(layers)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    log(f"config 6: seed {args.seed}, {layers} layers, {num_pages} pages per pool, {kv} KV")
+    k_pools = [fill_pool(torch, num_pages * PAGE, kv, gen, dev) for _ in range(layers)]
+    v_pools = [fill_pool(torch, num_pages * PAGE, kv, gen, dev) for _ in range(layers)]
+
+    def w(rows, cols, s):  # BF16 weights [rows, cols], N(0, s^2)
+        return (torch.randn((rows, cols), generator=gen, device=dev) * s).to(torch.bfloat16)
+
+    def vec(n, base, s):
+        return base + s * torch.randn(n, generator=gen, device=dev)
+
+    Wl = []
+    for _ in range(layers):
+        Wl.append(dict(inorm=vec(H, 1.0, 0.1), pnorm=vec(H, 1.0, 0.1),
+                       q=w(QD, H, 0.04), k=w(KVD, H, 0.04), v=w(KVD, H, 0.04),
+                       bq=vec(QD, 0.0, 0.1), bk=vec(KVD, 0.0, 0.1), bv=vec(KVD, 0.0, 0.1),
+                       o=w(H, QD, 0.03), g=w(I, H, 0.03), u=w(I, H, 0.03), d=w(H, I, 0.015)))
+    M = [{n: ie.matrix(t[n]) for n in ("q", "k", "v", "o", "g", "u", "d")} for t in Wl]
+    E = w(V, H, 1.0)
+    m_e = ie.matrix(E)
+    final_norm = vec(H, 1.0, 0.1)
+    ids = torch.from_numpy(rng.integers(0, V, B).astype(np.int32)).to(dev)
+    x = torch.empty((B, H), device=dev)
+    xn = torch.empty((B, H), device=dev)
+    q = torch.empty((B, QD), device=dev)
+    k = torch.empty((B, KVD), device=dev)
+    v = torch.empty((B, KVD), device=dev)
+    attn = torch.empty((B, QD), device=dev)
+    mid = torch.empty((B, I), device=dev)
+    logits = torch.empty((B, V), device=dev)
+    table = ie.rope_table(4096, HD, THETA).to(dev)
+    d_pos = torch.from_numpy((lens - 1).astype(np.int32)).to(dev)
+    d_seq = torch.arange(B, dtype=torch.int32, device=dev)
+    ct = args.chunk_tokens or ie.attention_chunk_tokens(B, 4096, KV_CODES[kv])
+    nc = ie.attention_chunks(4096, ct)
+    ws = ie.attention_workspace(B, NH, HD, nc)
+    if not ie.rope_cache_attention_supported(KV_CODES[kv], NH, NKV, HD, ct):
+        sys.exit("config 6 needs the one-launch decode step (16-bit KV)")
+    eps = 1e-6
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        ie.embedding(x, ids, m_e)
+        for l in range(layers):
+            t, m = Wl[l], M[l]
+            ie.rmsnorm(xn, x, t["inorm"], eps)
+            ie.matmul(q, xn, m["q"], t["bq"])
+            ie.matmul(k, xn, m["k"], t["bk"])
+            ie.matmul(v, xn, m["v"], t["bv"])
+            ie.rope_cache_attention(attn, q, k, v, k_pools[l], v_pools[l], table, d_pos, d_seq,
+                                    tabs[l], max_pages, nc, ct, ws, NH, NKV, HD)
+            ie.matmul(x, attn, m["o"], accumulate=True)
+            ie.rmsnorm(xn, x, t["pnorm"], eps)
+            ie.gate_up_silu(mid, xn, m["g"], m["u"])
+            ie.matmul(x, mid, m["d"], accumulate=True)
+        ie.rmsnorm(xn, x, final_norm, eps)
+        ie.matmul(logits, xn, m_e)
+
+    ms = time_steps(torch, step, args.steps, args.warmup, stream)
+    assert bool(torch.isfinite(logits).all()), "non-finite logits"
+    w_bytes = 2 * (QD * H + 2 * KVD * H + H * QD + 2 * I * H + H * I)
+    kv_bytes = decode_bytes(lens, KV_BYTES[kv])
+    nbytes = layers * (w_bytes + kv_bytes) + 2 * V * H + 4 * B * V
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "decode step (24-layer Qwen2.5-0.5B shape, batch 64) tok/s, 1 GPU",
+        "value": round(B / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": kv, "data": "synthetic",
+        "config": {"workload": "config 6: 24 layers x (rmsnorm, q/k/v, RoPE+append+attention, "
+                               "o_proj, rmsnorm, gate/up+SiLU, down) + final norm + tied LM "
+                               "head, batch 64, L~U[128,4096], random BF16 weights",
+                   "kv_dtype": kv, "chunk_tokens": ct, "num_chunks": nc, "seed": args.seed},
+        "us_per_layer": round((ms * 1e3) / layers, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "the whole step (one graph replay)",
+                     "us_per_launch": round(ms * 1e3, 3)},
+        "algorithmic_bytes_per_step": nbytes,
+        "bytes_note": "weights once per step, KV as config 3 per layer, the logits written; "
+                      "activations (under 3%) not counted",
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5, 6])
     ap.add_argument("--kv", choices=list(KV_CODES), default=None)
     ap.add_argument("--chunk-tokens", type=int, default=None)
     ap.add_argument("--layers", type=int, default=8)
@@ -664,7 +767,8 @@ def main():
         print(json.dumps({"measured_copy_gbs": copy_probe(torch), "copy_bytes": 2 << 30}),
               flush=True)
         return
-    res = {2: bench_append, 3: bench_decode, 4: bench_long, 5: bench_mixed}[args.config](
+    res = {2: bench_append, 3: bench_decode, 4: bench_long, 5: bench_mixed,
+           6: bench_model}[args.config](
         args, torch, ie, O)
     if args.probe:
         res["measured_copy_gbs"] = copy_probe(torch)

@@ -8,7 +8,7 @@
 // DeviceMatrix). Activations are f32.
 //
 // matmul_mfma_kernel: y[t][o] (+)= (sum_k W[o][k] x[t][k]) * s[o] + bias[o] on
-// v_mfma_f32_16x16x32_bf16. A workgroup owns a 16-row x 16-token output tile:
+// v_mfma_f32_16x16x32_bf16, in 16-row x 16-token output tiles:
 //   D[16 rows x 16 tokens] = W[16 x K] . x^T[K x 16]
 // The weights enter the MFMA exactly (BF16 as stored; INT8 values widened to
 // bf16, exact for |q| <= 127). Each activation is split into three bf16
@@ -16,19 +16,21 @@
 // at most 16, then 8, significant bits), and each block is multiplied three
 // times, so every product is the f32-exact w * x. Only the summation order
 // differs from the CPU's: the results agree to float32 rounding of the sum.
-// The 4 waves of a workgroup take interleaved 32-wide K blocks and their
-// partial tiles are added through LDS in wave order, so results do not depend
-// on scheduling. At decode batch sizes this gives rows/16 x T/16 workgroups
-// (224 for 896 rows and 64 tokens, 1,216 for the 4,864-row gate/up).
+// The 8 waves of a workgroup take interleaved 32-wide K blocks and their
+// partial tiles are added through LDS in a fixed order, so results do not
+// depend on scheduling. Larger launches take several tiles per workgroup
+// (see launch_matmul).
 // Lane (g, r) of a tile: A = W[row r][k + 8g .. +8], B = x[token r][k + 8g ..
 // +8]; the result lane holds rows 4g .. 4g+3 of token r.
+#include <algorithm>
+
 #include "common.hpp"
 #include "mfma.hpp"
 
 namespace iehip {
 namespace {
 
-constexpr int kMmWaves = 4;  // K split of a 16 x 16 output tile
+constexpr int kMmWaves = 8;  // waves of a workgroup, splitting K
 
 using bf16 = __bf16;
 
@@ -73,59 +75,103 @@ __device__ __forceinline__ f32x4 mma3(bf16x8 a, bf16x8 bh, bf16x8 bm, bf16x8 bl,
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
 // GATE: out = silu(x . Wg^T * sg) * (x . Wu^T * su) (gate_up_silu); otherwise
-// y (+)= x . W^T * s + bias. cols % 8 == 0; the K tail past cols is zero.
-template <bool GATE>
+// y (+)= x . W^T * s + bias. A workgroup owns RT x TT tiles of 16 rows x 16
+// tokens: each weight fragment is loaded once per K block and used for all TT
+// token tiles (so the weights are read once per launch when T <= 16 TT), each
+// activation fragment split once and used for all RT row tiles. cols % 8 == 0;
+// the K tail past cols is zero.
+template <bool GATE, int RT, int TT>
 __global__ void __launch_bounds__(64 * kMmWaves)
 matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const void* __restrict__ w,
                    const float* __restrict__ scale, const void* __restrict__ w2,
                    const float* __restrict__ scale2, const float* __restrict__ bias, int int8,
                    int T, int rows, int cols, int accumulate) {
-  __shared__ f32x4 red[GATE ? 2 : 1][kMmWaves - 1][64];
+  constexpr int NA = GATE ? 2 : 1, NT = NA * RT * TT;
+  static_assert(NT <= 16, "at most 16 accumulator tiles (64 KB of LDS for the reduction)");
+  __shared__ f32x4 red[kMmWaves / 2][NT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const int row0 = blockIdx.x * 16, tok0 = blockIdx.y * 16;
-  const size_t wrow = size_t(min(row0 + r, rows - 1)) * cols;     // rows past the end: last row
-  const float* xrow = x + size_t(min(tok0 + r, T - 1)) * cols;   // tokens likewise
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = acc;
+  const int row0 = blockIdx.x * 16 * RT, tok0 = blockIdx.y * 16 * TT;
+  size_t wrow[RT];
+#pragma unroll
+  for (int i = 0; i < RT; ++i) wrow[i] = size_t(min(row0 + 16 * i + r, rows - 1)) * cols;
+  const float* xrow[TT];
+#pragma unroll
+  for (int j = 0; j < TT; ++j) xrow[j] = x + size_t(min(tok0 + 16 * j + r, T - 1)) * cols;
+  f32x4 acc[NA][RT][TT];
+#pragma unroll
+  for (int n = 0; n < NA; ++n)
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int j = 0; j < TT; ++j) acc[n][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int kb = 32 * wave; kb < cols; kb += 32 * kMmWaves) {
     const int k = kb + 8 * g;
-    bf16x8 a = {}, a2 = {}, bh = {}, bm = {}, bl = {};
-    if (k < cols) {
-      a = load_weights(w, int8, wrow + k);
-      if constexpr (GATE) a2 = load_weights(w2, int8, wrow + k);
-      const float4* xp = reinterpret_cast<const float4*>(xrow + k);
-      split3(xp[0], xp[1], bh, bm, bl);
+    const bool kin = k < cols;
+    bf16x8 a[NA][RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      a[0][i] = kin ? load_weights(w, int8, wrow[i] + k) : bf16x8{};
+      if constexpr (GATE) a[NA - 1][i] = kin ? load_weights(w2, int8, wrow[i] + k) : bf16x8{};
     }
-    acc = mma3(a, bh, bm, bl, acc);
-    if constexpr (GATE) acc2 = mma3(a2, bh, bm, bl, acc2);
+#pragma unroll
+    for (int j = 0; j < TT; ++j) {
+      bf16x8 bh = {}, bm = {}, bl = {};
+      if (kin) {
+        const float4* xp = reinterpret_cast<const float4*>(xrow[j] + k);
+        split3(xp[0], xp[1], bh, bm, bl);
+      }
+#pragma unroll
+      for (int n = 0; n < NA; ++n)
+#pragma unroll
+        for (int i = 0; i < RT; ++i) acc[n][i][j] = mma3(a[n][i], bh, bm, bl, acc[n][i][j]);
+    }
   }
-  // Partial tiles of waves 1..3 through LDS, added to wave 0's in wave order.
-  if (wave > 0) {
-    red[0][wave - 1][lane] = acc;
-    if constexpr (GATE) red[GATE ? 1 : 0][wave - 1][lane] = acc2;
+  // The waves' partial tiles summed through LDS in a fixed tree (waves 4-7
+  // into 0-3, 2-3 into 0-1, 1 into 0), so results do not depend on timing.
+#pragma unroll
+  for (int half = kMmWaves / 2; half >= 1; half /= 2) {
+    if (wave >= half && wave < 2 * half) {
+#pragma unroll
+      for (int n = 0; n < NA; ++n)
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int j = 0; j < TT; ++j) red[wave - half][(n * RT + i) * TT + j][lane] = acc[n][i][j];
+    }
+    __syncthreads();
+    if (wave < half) {
+#pragma unroll
+      for (int n = 0; n < NA; ++n)
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int j = 0; j < TT; ++j) acc[n][i][j] += red[wave][(n * RT + i) * TT + j][lane];
+    }
+    __syncthreads();
   }
-  __syncthreads();
   if (wave > 0) return;
 #pragma unroll
-  for (int v = 0; v < kMmWaves - 1; ++v) {
-    acc += red[0][v][lane];
-    if constexpr (GATE) acc2 += red[GATE ? 1 : 0][v][lane];
-  }
-  const int tok = tok0 + r;
-  if (tok >= T) return;
-  float* yt = y + size_t(tok) * rows;
+  for (int j = 0; j < TT; ++j) {
+    const int tok = tok0 + 16 * j + r;
+    if (tok >= T) break;
+    float* yt = y + size_t(tok) * rows;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = row0 + 4 * g + i;
-    if (row >= rows) break;
-    float v = acc[i] * (int8 ? scale[row] : 1.0f);
-    if constexpr (GATE) {
-      v = silu(v) * (acc2[i] * (int8 ? scale2[row] : 1.0f));
-    } else {
-      if (bias) v += bias[row];
-      if (accumulate) v += yt[row];
+    for (int i = 0; i < RT; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = row0 + 16 * i + 4 * g + e;
+        if (row >= rows) break;
+        float v = acc[0][i][j][e] * (int8 ? scale[row] : 1.0f);
+        if constexpr (GATE) {
+          v = silu(v) * (acc[NA - 1][i][j][e] * (int8 ? scale2[row] : 1.0f));
+        } else {
+          if (bias) v += bias[row];
+          if (accumulate) v += yt[row];
+        }
+        yt[row] = v;
+      }
     }
-    yt[row] = v;
   }
 }
 
@@ -188,14 +234,48 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
                           (w2 ? reinterpret_cast<uintptr_t>(w2->data) : 0);
   if (align & (w.int8 ? 7 : 15))
     return fail(IE_HIP_EINVAL, std::string(who) + ": x and the weights must be 16-byte aligned");
-  const dim3 grid((w.rows + 15) / 16, (T + 15) / 16), block(64 * kMmWaves);
+  // Tiles per workgroup, from the count of 16 x 16 output tiles (measured on
+  // MI355X at 64 tokens): below 4 per compute unit (q/k/v/o and down at 896
+  // rows), one tile per workgroup keeps every unit busy; from 4 per unit
+  // (gate/up's 4,864 rows) two row tiles share each activation fragment;
+  // from 64 per unit (the 151,936-row LM head) 4 x 4 tiles read each weight
+  // once and each activation fragment a quarter as often. LM head at 64
+  // tokens: 366 -> 172 us; the others are slower with larger tiles.
+  const int cus = device_compute_units();
+  const int64_t tiles = int64_t((w.rows + 15) / 16) * ((T + 15) / 16);
+  const int RT = tiles >= 64 * int64_t(cus) ? 4 : tiles >= 4 * int64_t(cus) ? 2 : 1;
+  const int tok_tiles = (T + 15) / 16;  // kernels exist for 1, 2 and 4 token tiles
+  const int TT = tiles < 64 * int64_t(cus) ? 1 : tok_tiles > 2 ? 4 : tok_tiles;
+  const dim3 grid((w.rows + 16 * RT - 1) / (16 * RT), (T + 16 * TT - 1) / (16 * TT));
+  const dim3 block(64 * kMmWaves);
   if (grid.y > 65535) return fail(IE_HIP_EINVAL, std::string(who) + ": too many tokens");
-  if (gate)
-    hipLaunchKernelGGL(matmul_mfma_kernel<true>, grid, block, 0, stream, y, x, w.data, w.scale,
-                       w2->data, w2->scale, nullptr, w.int8, T, w.rows, w.cols, 0);
-  else
-    hipLaunchKernelGGL(matmul_mfma_kernel<false>, grid, block, 0, stream, y, x, w.data, w.scale,
-                       nullptr, nullptr, bias, w.int8, T, w.rows, w.cols, accumulate);
+  const void* w2d = gate ? w2->data : nullptr;
+  const float* s2 = gate ? w2->scale : nullptr;
+#define IE_MM_LAUNCH(G, R, C)                                                                    \
+  hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C>), grid, block, 0, stream, y, x, w.data,        \
+                     w.scale, w2d, s2, bias, w.int8, T, w.rows, w.cols, accumulate)
+#define IE_MM_TT(G, R)            \
+  if (TT == 4)                    \
+    IE_MM_LAUNCH(G, R, 4);        \
+  else if (TT == 2)               \
+    IE_MM_LAUNCH(G, R, 2);        \
+  else                            \
+    IE_MM_LAUNCH(G, R, 1);
+  if (gate) {  // two weight matrices: at most 2 row tiles
+    if (RT >= 2) {
+      IE_MM_TT(true, 2)
+    } else {
+      IE_MM_TT(true, 1)
+    }
+  } else if (RT == 4) {
+    IE_MM_TT(false, 4)
+  } else if (RT == 2) {
+    IE_MM_TT(false, 2)
+  } else {
+    IE_MM_TT(false, 1)
+  }
+#undef IE_MM_TT
+#undef IE_MM_LAUNCH
   return check_launch(who);
 }
 

@@ -78,6 +78,10 @@ MATMULS = [
     (64, 896, 4864, False, True),    # down_proj into the residual
     (37, 130, 104, True, True),      # ragged: rows % 16, cols % 32, T % 16 all nonzero
     (300, 896, 896, True, False),    # a prompt chunk
+    (64, 9000, 128, False, True),    # 2 row tiles per workgroup (>= 4 tiles per compute unit)
+    (40, 120000, 32, True, False),   # 4 x 4 tiles (>= 64 per unit), 3 token tiles rounded to 4
+    (64, 70000, 64, False, True),    # 4 x 4 tiles, every token in one workgroup
+    (20, 210000, 16, True, False),   # 4 x 2 tiles
 ]
 
 
