@@ -626,7 +626,8 @@ def bench_model(args, torch, ie, O):
     random BF16 weights, one new token for each of config 3's 64 rows (L ~ U[128, 4096],
     f16 KV, shuffled 16-token pages, one pool pair per layer). Per layer: rmsnorm,
     q/k/v, RoPE + paged append + attention (one launch), o_proj into the residual,
-    rmsnorm, gate/up + SiLU, down into the residual; then the final norm and the logits
+    rmsnorm, gate/up + SiLU, down into the residual (q/k/v in one launch); then the final
+    norm and the logits
     of every row (src/cuda/cuda_runner.cu:418-470)."""
     dev = torch.device("cuda:0")
     kv = args.kv or "f16"
@@ -655,7 +656,10 @@ def bench_model(args, torch, ie, O):
                        q=w(QD, H, 0.04), k=w(KVD, H, 0.04), v=w(KVD, H, 0.04),
                        bq=vec(QD, 0.0, 0.1), bk=vec(KVD, 0.0, 0.1), bv=vec(KVD, 0.0, 0.1),
                        o=w(H, QD, 0.03), g=w(I, H, 0.03), u=w(I, H, 0.03), d=w(H, I, 0.015)))
-    M = [{n: ie.matrix(t[n]) for n in ("q", "k", "v", "o", "g", "u", "d")} for t in Wl]
+    for t in Wl:  # Wq, Wk, Wv stacked for the one-launch q/k/v projection
+        t["qkv"] = torch.cat([t["q"], t["k"], t["v"]]).contiguous()
+        t["bqkv"] = torch.cat([t["bq"], t["bk"], t["bv"]]).contiguous()
+    M = [{n: ie.matrix(t[n]) for n in ("qkv", "o", "g", "u", "d")} for t in Wl]
     E = w(V, H, 1.0)
     m_e = ie.matrix(E)
     final_norm = vec(H, 1.0, 0.1)
@@ -684,9 +688,7 @@ def bench_model(args, torch, ie, O):
         for l in range(layers):
             t, m = Wl[l], M[l]
             ie.rmsnorm(xn, x, t["inorm"], eps)
-            ie.matmul(q, xn, m["q"], t["bq"])
-            ie.matmul(k, xn, m["k"], t["bk"])
-            ie.matmul(v, xn, m["v"], t["bv"])
+            ie.qkv_proj(q, k, v, xn, m["qkv"], t["bqkv"])
             ie.rope_cache_attention(attn, q, k, v, k_pools[l], v_pools[l], table, d_pos, d_seq,
                                     tabs[l], max_pages, nc, ct, ws, NH, NKV, HD)
             ie.matmul(x, attn, m["o"], accumulate=True)

@@ -218,6 +218,14 @@ int ie_hip_rmsnorm(float* y, const float* x, const float* weight, int T, int dim
 int ie_hip_matmul(float* y, const float* x, ie_matrix w, const float* bias, int T, int accumulate,
                   hipStream_t stream);
 
+/* The q, k and v projections in one launch: W_qkv is Wq, Wk and Wv stacked
+ * ([q_dim + 2 kv_dim, cols]) and b_qkv their biases (or NULL); rows go to
+ * q [T, q_dim], k [T, kv_dim] and v [T, kv_dim]. The same results as three
+ * ie_hip_matmul calls (src/cuda/cuda_runner.cu:436-438); no counterpart in the
+ * reference, which launches the three. */
+int ie_hip_qkv_proj(float* q, float* k, float* v, const float* x, ie_matrix w_qkv,
+                    const float* b_qkv, int T, int q_dim, int kv_dim, hipStream_t stream);
+
 /* out[t, o] = silu(x[t] . Wg[o] * sg[o]) * (x[t] . Wu[o] * su[o]), silu(v) =
  * v / (1 + exp(-v)): the MLP's gate and up projections and the SwiGLU in one
  * launch. Wg and Wu of the same shape and format. Replaces gate_up_silu

@@ -114,6 +114,10 @@ inline void matmul(float* y, const float* x, const ie_matrix& w, const float* bi
                    bool accumulate, hipStream_t stream) {
   check(ie_hip_matmul(y, x, w, bias, T, accumulate ? 1 : 0, stream));
 }
+inline void qkv_proj(float* q, float* k, float* v, const float* x, const ie_matrix& w_qkv,
+                     const float* b_qkv, int T, int q_dim, int kv_dim, hipStream_t stream) {
+  check(ie_hip_qkv_proj(q, k, v, x, w_qkv, b_qkv, T, q_dim, kv_dim, stream));
+}
 inline void gate_up_silu(float* out, const float* x, const ie_matrix& wg, const ie_matrix& wu,
                          int T, hipStream_t stream) {
   check(ie_hip_gate_up_silu(out, x, wg, wu, T, stream));

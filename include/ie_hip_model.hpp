@@ -4,7 +4,7 @@
  * CudaEngine forward (src/cuda/cuda_runner.cu:418-470):
  *   embed(ids)              x = E[ids]                 (embedding)
  *   per layer, around the engine's RoPE + paged append + attention:
- *     before_attention      xn = rmsnorm(x); q, k, v = xn . W^T + b
+ *     before_attention      xn = rmsnorm(x); q, k, v = xn . W^T + b (one launch)
  *     after_attention       x += attn . Wo^T; xn = rmsnorm(x);
  *                           mid = silu(xn . Wg^T) * (xn . Wu^T); x += mid . Wd^T
  *   logits(rows)            xn = rmsnorm(x); logits = xn[rows] . E_out^T
@@ -64,13 +64,20 @@ class DecoderModel {
       Layer l;
       l.input_norm = upload(h.input_norm, H);
       l.post_norm = upload(h.post_norm, H);
-      l.wq = upload_matrix(h.wq, QD, H);
-      l.wk = upload_matrix(h.wk, KVD, H);
-      l.wv = upload_matrix(h.wv, KVD, H);
+      if (h.wq.size() != size_t(QD) * H || h.wk.size() != size_t(KVD) * H ||
+          h.wv.size() != size_t(KVD) * H || h.bq.size() != size_t(QD) ||
+          h.bk.size() != size_t(KVD) || h.bv.size() != size_t(KVD))
+        throw std::runtime_error("DecoderModel: q/k/v weight of the wrong size");
+      // Wq, Wk, Wv stacked (and their biases), for one q/k/v launch.
+      std::vector<uint16_t> wqkv(h.wq);
+      wqkv.insert(wqkv.end(), h.wk.begin(), h.wk.end());
+      wqkv.insert(wqkv.end(), h.wv.begin(), h.wv.end());
+      std::vector<float> bqkv(h.bq);
+      bqkv.insert(bqkv.end(), h.bk.begin(), h.bk.end());
+      bqkv.insert(bqkv.end(), h.bv.begin(), h.bv.end());
+      l.wqkv = upload_matrix(wqkv, QD + 2 * KVD, H);
+      l.bqkv = upload(bqkv, bqkv.size());
       l.wo = upload_matrix(h.wo, H, QD);
-      l.bq = upload(h.bq, QD);
-      l.bk = upload(h.bk, KVD);
-      l.bv = upload(h.bv, KVD);
       l.w_gate = upload_matrix(h.w_gate, I, H);
       l.w_up = upload_matrix(h.w_up, I, H);
       l.w_down = upload_matrix(h.w_down, H, I);
@@ -93,9 +100,8 @@ class DecoderModel {
       check_rows(rows);
       const Layer& L = layers_.at(l);
       rmsnorm(xn_, x_, L.input_norm, rows, shape_.hidden, shape_.rms_eps, s);
-      matmul(engine.q(), xn_, L.wq, L.bq, rows, false, s);
-      matmul(engine.k(), xn_, L.wk, L.bk, rows, false, s);
-      matmul(engine.v(), xn_, L.wv, L.bv, rows, false, s);
+      qkv_proj(engine.q(), engine.k(), engine.v(), xn_, L.wqkv, L.bqkv, rows, kv_.q_dim(),
+               kv_.kv_dim(), s);
     };
     b.after_attention = [this, &engine](int l, int rows, hipStream_t s) {
       const Layer& L = layers_.at(l);
@@ -135,8 +141,8 @@ class DecoderModel {
 
  private:
   struct Layer {
-    const float *input_norm, *post_norm, *bq, *bk, *bv;
-    ie_matrix wq, wk, wv, wo, w_gate, w_up, w_down;
+    const float *input_norm, *post_norm, *bqkv;
+    ie_matrix wqkv, wo, w_gate, w_up, w_down;
   };
 
   void check_rows(int rows) const {

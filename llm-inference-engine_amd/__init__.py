@@ -75,6 +75,7 @@ _SIGS = {
     "ie_hip_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     "ie_hip_matmul": (_i, [_vp, _vp, Matrix, _vp, _i, _i, _vp]),
     "ie_hip_gate_up_silu": (_i, [_vp, _vp, Matrix, Matrix, _i, _vp]),
+    "ie_hip_qkv_proj": (_i, [_vp, _vp, _vp, _vp, Matrix, _vp, _i, _i, _i, _vp]),
     "ie_pages_create": (_vp, [_i, _i, _i]),
     "ie_pages_destroy": (None, [_vp]),
     "ie_pages_open_sequence": (_i, [_vp]),
@@ -271,6 +272,13 @@ def matmul(y, x, w: Matrix, bias=None, accumulate: bool = False, stream=None) ->
     """y (+)= x . W^T * scale + bias (src/cuda/kernels.cuh:55-62)."""
     _check(lib().ie_hip_matmul(_ptr(y), _ptr(x), w, _ptr(bias), x.numel() // w.cols,
                                int(accumulate), _stream(stream)))
+
+
+def qkv_proj(q, k, v, x, w_qkv: Matrix, b_qkv=None, stream=None) -> None:
+    """q, k, v = x . [Wq; Wk; Wv]^T + [bq; bk; bv] in one launch."""
+    q_dim, kv_dim = q.shape[-1], k.shape[-1]
+    _check(lib().ie_hip_qkv_proj(_ptr(q), _ptr(k), _ptr(v), _ptr(x), w_qkv, _ptr(b_qkv),
+                                 x.numel() // w_qkv.cols, q_dim, kv_dim, _stream(stream)))
 
 
 def gate_up_silu(out, x, w_gate: Matrix, w_up: Matrix, stream=None) -> None:

@@ -80,12 +80,21 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 // token tiles (so the weights are read once per launch when T <= 16 TT), each
 // activation fragment split once and used for all RT row tiles. cols % 8 == 0;
 // the K tail past cols is zero.
+// Outputs: rows [0, split0) go to y ([T, split0]), rows [split0, split1) to y1
+// ([T, split1 - split0]) and the rest to y2 ([T, rows - split1]); a plain
+// matmul has split0 = split1 = rows.
+struct RowSplit {
+  float* y1;
+  float* y2;
+  int split0, split1;
+};
+
 template <bool GATE, int RT, int TT>
 __global__ void __launch_bounds__(64 * kMmWaves)
 matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const void* __restrict__ w,
                    const float* __restrict__ scale, const void* __restrict__ w2,
                    const float* __restrict__ scale2, const float* __restrict__ bias, int int8,
-                   int T, int rows, int cols, int accumulate) {
+                   int T, int rows, int cols, int accumulate, RowSplit out) {
   constexpr int NA = GATE ? 2 : 1, NT = NA * RT * TT;
   static_assert(NT <= 16, "at most 16 accumulator tiles (64 KB of LDS for the reduction)");
   __shared__ f32x4 red[kMmWaves / 2][NT][64];
@@ -155,7 +164,6 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
   for (int j = 0; j < TT; ++j) {
     const int tok = tok0 + 16 * j + r;
     if (tok >= T) break;
-    float* yt = y + size_t(tok) * rows;
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
 #pragma unroll
@@ -163,13 +171,20 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
         const int row = row0 + 16 * i + 4 * g + e;
         if (row >= rows) break;
         float v = acc[0][i][j][e] * (int8 ? scale[row] : 1.0f);
+        float* dst;
+        if (row < out.split0)
+          dst = y + size_t(tok) * out.split0 + row;
+        else if (row < out.split1)
+          dst = out.y1 + size_t(tok) * (out.split1 - out.split0) + (row - out.split0);
+        else
+          dst = out.y2 + size_t(tok) * (rows - out.split1) + (row - out.split1);
         if constexpr (GATE) {
           v = silu(v) * (acc[NA - 1][i][j][e] * (int8 ? scale2[row] : 1.0f));
         } else {
           if (bias) v += bias[row];
-          if (accumulate) v += yt[row];
+          if (accumulate) v += *dst;
         }
-        yt[row] = v;
+        *dst = v;
       }
     }
   }
@@ -218,7 +233,9 @@ int check_matrix(const ie_matrix& m, const char* who) {
 }
 
 int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const ie_matrix* w2,
-                  const float* bias, int T, int accumulate, hipStream_t stream, const char* who) {
+                  const float* bias, int T, int accumulate, hipStream_t stream, const char* who,
+                  RowSplit split = RowSplit{nullptr, nullptr, 0, 0}) {
+  if (split.split0 == 0 && split.split1 == 0) split.split0 = split.split1 = w.rows;
   if (int rc = check_matrix(w, who)) return rc;
   if (w2) {
     if (int rc = check_matrix(*w2, who)) return rc;
@@ -253,7 +270,7 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   const float* s2 = gate ? w2->scale : nullptr;
 #define IE_MM_LAUNCH(G, R, C)                                                                    \
   hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C>), grid, block, 0, stream, y, x, w.data,        \
-                     w.scale, w2d, s2, bias, w.int8, T, w.rows, w.cols, accumulate)
+                     w.scale, w2d, s2, bias, w.int8, T, w.rows, w.cols, accumulate, split)
 #define IE_MM_TT(G, R)            \
   if (TT == 4)                    \
     IE_MM_LAUNCH(G, R, 4);        \
@@ -310,6 +327,17 @@ extern "C" int ie_hip_matmul(float* y, const float* x, ie_matrix w, const float*
                              int accumulate, hipStream_t stream) {
   clear_error();
   return launch_matmul(false, y, x, w, nullptr, bias, T, accumulate, stream, "matmul");
+}
+
+extern "C" int ie_hip_qkv_proj(float* q, float* k, float* v, const float* x, ie_matrix w_qkv,
+                               const float* b_qkv, int T, int q_dim, int kv_dim,
+                               hipStream_t stream) {
+  clear_error();
+  if (q_dim <= 0 || kv_dim <= 0 || w_qkv.rows != q_dim + 2 * kv_dim)
+    return fail(IE_HIP_EINVAL, "qkv_proj: weight rows must be q_dim + 2 kv_dim");
+  if (T > 0 && (!q || !k || !v)) return fail(IE_HIP_EINVAL, "qkv_proj: null pointer");
+  return launch_matmul(false, q, x, w_qkv, nullptr, b_qkv, T, 0, stream, "qkv_proj",
+                       RowSplit{k, v, q_dim, q_dim + kv_dim});
 }
 
 extern "C" int ie_hip_gate_up_silu(float* out, const float* x, ie_matrix w_gate, ie_matrix w_up,

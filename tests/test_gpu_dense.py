@@ -122,6 +122,27 @@ def test_gate_up_silu(ie, dev, int8, T):
     assert rel_err(out.cpu().numpy(), want) <= REL
 
 
+@pytest.mark.parametrize("int8", [False, True])
+@pytest.mark.parametrize("T", [1, 64, 300])
+def test_qkv_proj_matches_three_matmuls(ie, dev, int8, T):
+    """The one-launch q/k/v projection: Wq, Wk, Wv stacked, each output to its own buffer."""
+    rng = np.random.default_rng(20 + T)
+    H, QD, KVD = 896, 896, 128
+    x = rng.standard_normal((T, H), dtype=np.float32)
+    w32 = rng.standard_normal((QD + 2 * KVD, H), dtype=np.float32) * np.float32(0.05)
+    b = rng.standard_normal(QD + 2 * KVD, dtype=np.float32)
+    m, keep, (w, fmt, s) = dev_weights(ie, dev, w32, int8)
+    q = torch.full((T, QD), float("nan"), device=dev)
+    k = torch.full((T, KVD), float("nan"), device=dev)
+    v = torch.full((T, KVD), float("nan"), device=dev)
+    ie.qkv_proj(q, k, v, torch.from_numpy(x).to(dev), m, torch.from_numpy(b).to(dev))
+    torch.cuda.synchronize()
+    want = O.matmul(x, w, fmt, s, b)
+    assert rel_err(q.cpu().numpy(), want[:, :QD]) <= REL
+    assert rel_err(k.cpu().numpy(), want[:, QD:QD + KVD]) <= REL
+    assert rel_err(v.cpu().numpy(), want[:, QD + KVD:]) <= REL
+
+
 def test_dense_argument_errors(ie, dev):
     x = torch.zeros((4, 12), device=dev)
     y = torch.zeros((4, 16), device=dev)
