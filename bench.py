@@ -656,12 +656,30 @@ def bench_model(args, torch, ie, O):
                        q=w(QD, H, 0.04), k=w(KVD, H, 0.04), v=w(KVD, H, 0.04),
                        bq=vec(QD, 0.0, 0.1), bk=vec(KVD, 0.0, 0.1), bv=vec(KVD, 0.0, 0.1),
                        o=w(H, QD, 0.03), g=w(I, H, 0.03), u=w(I, H, 0.03), d=w(H, I, 0.015)))
+    int8 = args.weights == "int8"
+
+    def mat(wb):  # BF16 weights, or INT8 with row scales (src/matrix.cpp:84-97)
+        if not int8:
+            return ie.matrix(wb), (wb,)
+        wf = wb.float()
+        amax = wf.abs().amax(dim=1)
+        sc = torch.where(amax > 0, amax / 127.0, torch.ones_like(amax))
+        q8 = torch.round(wf / sc[:, None]).clamp(-127, 127).to(torch.int8)
+        return ie.matrix(q8, sc), (q8, sc)
+
     for t in Wl:  # Wq, Wk, Wv stacked for the one-launch q/k/v projection
         t["qkv"] = torch.cat([t["q"], t["k"], t["v"]]).contiguous()
         t["bqkv"] = torch.cat([t["bq"], t["bk"], t["bv"]]).contiguous()
-    M = [{n: ie.matrix(t[n]) for n in ("qkv", "o", "g", "u", "d")} for t in Wl]
+    keep = []
+    M = []
+    for t in Wl:
+        mm = {}
+        for n in ("qkv", "o", "g", "u", "d"):
+            mm[n], kp_ = mat(t[n])
+            keep.append(kp_)
+        M.append(mm)
     E = w(V, H, 1.0)
-    m_e = ie.matrix(E)
+    m_e, keep_e = mat(E)
     final_norm = vec(H, 1.0, 0.1)
     ids = torch.from_numpy(rng.integers(0, V, B).astype(np.int32)).to(dev)
     x = torch.empty((B, H), device=dev)
@@ -700,9 +718,11 @@ def bench_model(args, torch, ie, O):
 
     ms = time_steps(torch, step, args.steps, args.warmup, stream)
     assert bool(torch.isfinite(logits).all()), "non-finite logits"
-    w_bytes = 2 * (QD * H + 2 * KVD * H + H * QD + 2 * I * H + H * I)
+    wb = 1 if int8 else 2  # bytes per weight, plus a 4-byte scale per row for INT8
+    w_bytes = wb * (QD * H + 2 * KVD * H + H * QD + 2 * I * H + H * I) + \
+        (4 * (QD + 2 * KVD + H + 2 * I + H) if int8 else 0)
     kv_bytes = decode_bytes(lens, KV_BYTES[kv])
-    nbytes = layers * (w_bytes + kv_bytes) + 2 * V * H + 4 * B * V
+    nbytes = layers * (w_bytes + kv_bytes) + wb * V * H + (4 * V if int8 else 0) + 4 * B * V
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {
         "metric": "decode step (24-layer Qwen2.5-0.5B shape, batch 64) tok/s, 1 GPU",
@@ -712,7 +732,8 @@ def bench_model(args, torch, ie, O):
         "config": {"workload": "config 6: 24 layers x (rmsnorm, q/k/v, RoPE+append+attention, "
                                "o_proj, rmsnorm, gate/up+SiLU, down) + final norm + tied LM "
                                "head, batch 64, L~U[128,4096], random BF16 weights",
-                   "kv_dtype": kv, "chunk_tokens": ct, "num_chunks": nc, "seed": args.seed},
+                   "kv_dtype": kv, "weights": args.weights, "chunk_tokens": ct,
+                   "num_chunks": nc, "seed": args.seed},
         "us_per_layer": round((ms * 1e3) / layers, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
@@ -737,6 +758,8 @@ def main():
     ap.add_argument("--seed", type=int, default=20263)
     ap.add_argument("--unfused", action="store_true",
                     help="config 4: RoPE + append and attention as two calls per layer")
+    ap.add_argument("--weights", choices=["bf16", "int8"], default="bf16",
+                    help="config 6: weight storage (INT8 with row scales, as --dtype int8)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true", help="config 2: rows-per-launch sweep")

@@ -8,14 +8,17 @@
  *     after_attention       x += attn . Wo^T; xn = rmsnorm(x);
  *                           mid = silu(xn . Wg^T) * (xn . Wu^T); x += mid . Wd^T
  *   logits(rows)            xn = rmsnorm(x); logits = xn[rows] . E_out^T
- * Weights are BF16 bits in the reference's layout (nn.Linear [out, in]);
- * the norms and biases f32. All work is enqueued on the engine's stream, so a
+ * Weights are BF16 bits in the reference's layout (nn.Linear [out, in]),
+ * stored on the device as BF16 or quantized to INT8; the norms and biases f32. All work is enqueued on the engine's stream, so a
  * decode step's layers are recorded into the engine's graphs with its
  * attention. Header-only. */
 #ifndef IE_HIP_MODEL_HPP_
 #define IE_HIP_MODEL_HPP_
 
+#include <algorithm>
+#include <cmath>
 #include <cstdint>
+#include <cstring>
 #include <stdexcept>
 #include <vector>
 
@@ -50,9 +53,13 @@ struct HostModel {
 class DecoderModel {
  public:
   /* Uploads the weights; `max_rows` bounds a step's rows (as the engine's
-   * max batch bounds a decode step, and the largest prompt chunk a prefill). */
-  DecoderModel(const KvConfig& kv, const ModelShape& shape, const HostModel& host, int max_rows)
-      : kv_(kv), shape_(shape), max_rows_(max_rows) {
+   * max batch bounds a decode step, and the largest prompt chunk a prefill).
+   * int8: every matrix, the embedding included, stored as INT8 with one scale
+   * per row, quantized as the reference's --dtype int8 does
+   * (src/weights.cpp:95-114, src/matrix.cpp:84-97). */
+  DecoderModel(const KvConfig& kv, const ModelShape& shape, const HostModel& host, int max_rows,
+               bool int8 = false)
+      : kv_(kv), shape_(shape), max_rows_(max_rows), int8_(int8) {
     const int H = shape.hidden, I = shape.intermediate, QD = kv.q_dim(), KVD = kv.kv_dim();
     if (int(host.layers.size()) != kv.num_layers)
       throw std::runtime_error("DecoderModel: layer count differs from the engine's");
@@ -156,15 +163,41 @@ class DecoderModel {
   }
   ie_matrix upload_matrix(const std::vector<uint16_t>& w, int rows, int cols) {
     if (w.size() != size_t(rows) * cols) throw std::runtime_error("DecoderModel: matrix of the wrong size");
-    uint16_t* d = mem_.alloc<uint16_t>(w.size());
-    check(hipMemcpy(d, w.data(), w.size() * sizeof(uint16_t), hipMemcpyHostToDevice),
-          "hipMemcpy(weights)");
-    return ie_matrix{d, nullptr, 0, rows, cols};
+    if (!int8_) {
+      uint16_t* d = mem_.alloc<uint16_t>(w.size());
+      check(hipMemcpy(d, w.data(), w.size() * sizeof(uint16_t), hipMemcpyHostToDevice),
+            "hipMemcpy(weights)");
+      return ie_matrix{d, nullptr, 0, rows, cols};
+    }
+    // Per row: s = max|w| / 127 (1 for a zero row), q = clamp(nearbyint(w / s)).
+    std::vector<int8_t> q(w.size());
+    std::vector<float> sc(rows);
+    for (int r = 0; r < rows; ++r) {
+      const uint16_t* row = w.data() + size_t(r) * cols;
+      float amax = 0.0f;
+      for (int i = 0; i < cols; ++i) amax = std::max(amax, std::fabs(bf16_value(row[i])));
+      const float s = amax > 0 ? amax / 127.0f : 1.0f;
+      sc[r] = s;
+      for (int i = 0; i < cols; ++i) {
+        const float v = std::nearbyint(bf16_value(row[i]) / s);
+        q[size_t(r) * cols + i] = int8_t(std::max(-127.0f, std::min(127.0f, v)));
+      }
+    }
+    int8_t* d = mem_.alloc<int8_t>(q.size());
+    check(hipMemcpy(d, q.data(), q.size(), hipMemcpyHostToDevice), "hipMemcpy(weights)");
+    return ie_matrix{d, upload(sc, sc.size()), 1, rows, cols};
+  }
+  static float bf16_value(uint16_t b) {
+    const uint32_t bits = uint32_t(b) << 16;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
   }
 
   KvConfig kv_;
   ModelShape shape_;
   int max_rows_;
+  bool int8_;
   DeviceMemory mem_;
   ie_matrix embed_{};
   const float* final_norm_ = nullptr;

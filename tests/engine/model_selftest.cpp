@@ -15,7 +15,10 @@
 // on both sides from inputs that already differ in the last float32 bits;
 // measured about 6e-5).
 //
-// usage: model_selftest f32|f16      exit status 0 when every check passes.
+// With `int8`, every matrix is stored as INT8 with row scales on both sides
+// (the reference's --dtype int8).
+//
+// usage: model_selftest f32|f16 [int8]      exit status 0 when every check passes.
 #include <cmath>
 #include <cstdio>
 #include <random>
@@ -45,16 +48,37 @@ void result(bool ok, const std::string& what) {
 struct Cpu {  // the reference's CPU forward on the oracle, over paged host pools
   const HostModel& m;
   int kv;
+  bool int8;
   std::vector<std::vector<unsigned char>> kp, vp;
-  Cpu(const HostModel& model, int kv_dtype, size_t pool_bytes)
-      : m(model), kv(kv_dtype), kp(kLayers, std::vector<unsigned char>(pool_bytes)),
+  Cpu(const HostModel& model, int kv_dtype, size_t pool_bytes, bool int8_weights)
+      : m(model), kv(kv_dtype), int8(int8_weights),
+        kp(kLayers, std::vector<unsigned char>(pool_bytes)),
         vp(kLayers, std::vector<unsigned char>(pool_bytes)) {}
+
+  // A matrix as the reference stores it for --dtype int8 (src/matrix.cpp:84-97).
+  struct Q8 {
+    std::vector<int8_t> q;
+    std::vector<float> s;
+  };
+  Q8 quantize(const std::vector<uint16_t>& w, int rows, int cols) {
+    std::vector<float> f(w.size());
+    for (size_t i = 0; i < w.size(); ++i) f[i] = orc_bf16_to_f32(w[i]);
+    Q8 r{std::vector<int8_t>(w.size()), std::vector<float>(rows)};
+    orc_quantize_i8(r.q.data(), r.s.data(), f.data(), rows, cols);
+    return r;
+  }
 
   std::vector<float> mm(const std::vector<float>& x, const std::vector<uint16_t>& w,
                         const std::vector<float>* b, int T, int rows, int cols) {
     std::vector<float> y(size_t(T) * rows);
-    orc_matmul(y.data(), x.data(), w.data(), ORC_W_BF16, nullptr, b ? b->data() : nullptr, T,
-               rows, cols, 8);
+    if (int8) {
+      const Q8 q = quantize(w, rows, cols);
+      orc_matmul(y.data(), x.data(), q.q.data(), ORC_W_I8, q.s.data(), b ? b->data() : nullptr,
+                 T, rows, cols, 8);
+    } else {
+      orc_matmul(y.data(), x.data(), w.data(), ORC_W_BF16, nullptr, b ? b->data() : nullptr, T,
+                 rows, cols, 8);
+    }
     return y;
   }
 
@@ -64,7 +88,14 @@ struct Cpu {  // the reference's CPU forward on the oracle, over paged host pool
             std::vector<float>& x, std::vector<float>& logits) {
     const int T = int(ids.size());
     x.assign(size_t(T) * H, 0.0f);
-    for (int t = 0; t < T; ++t) orc_row_to_f32(&x[size_t(t) * H], m.embed.data(), ORC_W_BF16, nullptr, H, ids[t]);
+    if (int8) {
+      const Q8 e = quantize(m.embed, V, H);
+      for (int t = 0; t < T; ++t)
+        orc_row_to_f32(&x[size_t(t) * H], e.q.data(), ORC_W_I8, e.s.data(), H, ids[t]);
+    } else {
+      for (int t = 0; t < T; ++t)
+        orc_row_to_f32(&x[size_t(t) * H], m.embed.data(), ORC_W_BF16, nullptr, H, ids[t]);
+    }
     std::vector<float> xn(x.size());
     for (int l = 0; l < kLayers; ++l) {
       const HostLayer& L = m.layers[l];
@@ -135,6 +166,7 @@ std::vector<T> download(const void* d, size_t n) {
 
 int main(int argc, char** argv) {
   const std::string kvs = argc > 1 ? argv[1] : "f32";
+  const bool int8 = argc > 2 && std::string(argv[2]) == "int8";
   const int kv = kvs == "f16" ? IE_KV_F16 : IE_KV_F32;
   const double tol = kv == IE_KV_F32 ? 1e-5 : 1e-3;
   std::mt19937 rng(20261201u);
@@ -144,10 +176,10 @@ int main(int argc, char** argv) {
   ModelShape shape;
   shape.vocab = V;
   try {
-    DecoderModel model(cfg, shape, host, /*max_rows=*/64);
+    DecoderModel model(cfg, shape, host, /*max_rows=*/64, int8);
     KvEngine eng(cfg, kMaxBatch, kMaxSeq, kPages, /*use_graphs=*/true, kv);
     eng.set_body(model.body(eng));
-    Cpu cpu(host, kv, eng.layer_pool_bytes());
+    Cpu cpu(host, kv, eng.layer_pool_bytes(), int8);
     float* d_logits = nullptr;
     check(hipMalloc(&d_logits, size_t(64) * V * sizeof(float)), "hipMalloc");
     std::uniform_int_distribution<int> tok(0, V - 1);

@@ -53,12 +53,12 @@ def test_model_driver_built_and_linked():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kv", ["f32", "f16"])
-def test_model_selftest(kv):
+@pytest.mark.parametrize("kv,weights", [("f32", "bf16"), ("f16", "bf16"), ("f32", "int8")])
+def test_model_selftest(kv, weights):
     """A 2-layer Qwen2 decoder (Qwen2.5-0.5B layer shape) through KvEngine + DecoderModel
     (include/ie_hip_model.hpp): prompts, decode graphs and a replay; after every step the
     residual stream and logits against the reference's CPU forward restated on the oracle."""
-    print(f"model_selftest {kv}", flush=True)
-    r = subprocess.run([MODEL_BIN, kv], capture_output=True, text=True, timeout=110)
+    print(f"model_selftest {kv} {weights}", flush=True)
+    r = subprocess.run([MODEL_BIN, kv, weights], capture_output=True, text=True, timeout=110)
     print(r.stdout[-6000:], r.stderr[-2000:], flush=True)
     assert r.returncode == 0 and " checks, 0 failures" in r.stdout
