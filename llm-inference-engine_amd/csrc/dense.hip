@@ -89,15 +89,15 @@ struct RowSplit {
   int split0, split1;
 };
 
-template <bool GATE, int RT, int TT>
-__global__ void __launch_bounds__(64 * kMmWaves)
+template <bool GATE, int RT, int TT, int W = kMmWaves>
+__global__ void __launch_bounds__(64 * W)
 matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const void* __restrict__ w,
                    const float* __restrict__ scale, const void* __restrict__ w2,
                    const float* __restrict__ scale2, const float* __restrict__ bias, int int8,
                    int T, int rows, int cols, int accumulate, RowSplit out) {
   constexpr int NA = GATE ? 2 : 1, NT = NA * RT * TT;
   static_assert(NT <= 16, "at most 16 accumulator tiles (64 KB of LDS for the reduction)");
-  __shared__ f32x4 red[kMmWaves / 2][NT][64];
+  __shared__ f32x4 red[W / 2][NT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int row0 = blockIdx.x * 16 * RT, tok0 = blockIdx.y * 16 * TT;
@@ -114,7 +114,7 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
     for (int i = 0; i < RT; ++i)
 #pragma unroll
       for (int j = 0; j < TT; ++j) acc[n][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = 32 * wave; kb < cols; kb += 32 * kMmWaves) {
+  for (int kb = 32 * wave; kb < cols; kb += 32 * W) {
     const int k = kb + 8 * g;
     const bool kin = k < cols;
     bf16x8 a[NA][RT];
@@ -139,7 +139,7 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
   // The waves' partial tiles summed through LDS in a fixed tree (waves 4-7
   // into 0-3, 2-3 into 0-1, 1 into 0), so results do not depend on timing.
 #pragma unroll
-  for (int half = kMmWaves / 2; half >= 1; half /= 2) {
+  for (int half = W / 2; half >= 1; half /= 2) {
     if (wave >= half && wave < 2 * half) {
 #pragma unroll
       for (int n = 0; n < NA; ++n)
@@ -264,13 +264,23 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   const int tok_tiles = (T + 15) / 16;  // kernels exist for 1, 2 and 4 token tiles
   const int TT = tiles < 64 * int64_t(cus) ? 1 : tok_tiles > 2 ? 4 : tok_tiles;
   const dim3 grid((w.rows + 16 * RT - 1) / (16 * RT), (T + 16 * TT - 1) / (16 * TT));
-  const dim3 block(64 * kMmWaves);
+  // 4 x 4 tiles hold ~140 registers a lane: in workgroups of 4 waves, three
+  // fit on a compute unit where one of 8 would (LM head at 64 tokens: 176 ->
+  // 149 us on MI355X).
+  const int waves = RT == 4 ? 4 : kMmWaves;
+  const dim3 block(64 * waves);
   if (grid.y > 65535) return fail(IE_HIP_EINVAL, std::string(who) + ": too many tokens");
   const void* w2d = gate ? w2->data : nullptr;
   const float* s2 = gate ? w2->scale : nullptr;
 #define IE_MM_LAUNCH(G, R, C)                                                                    \
-  hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C>), grid, block, 0, stream, y, x, w.data,        \
-                     w.scale, w2d, s2, bias, w.int8, T, w.rows, w.cols, accumulate, split)
+  do {                                                                                           \
+    if (R == 4)                                                                                  \
+      hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C, 4>), grid, block, 0, stream, y, x, w.data, \
+                         w.scale, w2d, s2, bias, w.int8, T, w.rows, w.cols, accumulate, split);  \
+    else                                                                                         \
+      hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C>), grid, block, 0, stream, y, x, w.data,    \
+                         w.scale, w2d, s2, bias, w.int8, T, w.rows, w.cols, accumulate, split);  \
+  } while (0)
 #define IE_MM_TT(G, R)            \
   if (TT == 4)                    \
     IE_MM_LAUNCH(G, R, 4);        \
