@@ -238,6 +238,66 @@ def cpu_baseline_long(O, k_pools, v_pools, tabs, q, L, kv, layers, budget_s=8.0)
             "ms_per_step": round(t * 1e3, 2), "tok_per_s": round(1 / t, 2)}
 
 
+def cpu_baseline_model(O, layer_bits, norms, embed_bits, x, kc, vc, pos, layers, reps=3):
+    """Config 6 on the CPU with the reference's own code (oracle/_ref: src/matrix.cpp AVX2
+    matmul, src/ops.cpp rmsnorm and attention, its thread pool): one layer's dense work for
+    the 64 rows (rmsnorm, q/k/v, o_proj, rmsnorm, gate/up, SiLU in numpy, down; median of
+    `reps`), the attention of a sample of rows over their contexts (gathered to contiguous
+    fp32 beforehand) scaled to all 64, both x 24 layers, plus the LM head once."""
+    import ctypes
+    cores = _cpu_threads(O)
+    R = O.ref()
+    R.ref_matrix_create.restype = ctypes.c_void_p
+    R.ref_matrix_create.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    R.ref_matrix_destroy.argtypes = [ctypes.c_void_p]
+    R.ref_matrix_matmul.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int]
+    mats = {n: (R.ref_matrix_create(w.ctypes.data, 1, w.shape[0], w.shape[1]), w.shape[0])
+            for n, w in layer_bits.items()}
+    B, H = x.shape
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    q_rows = np.random.default_rng(1).standard_normal((len(kc), QD), dtype=np.float32)
+
+    def mm(name, inp):
+        m, rows = mats[name]
+        y = np.empty((B, rows), np.float32)
+        R.ref_matrix_matmul(ptr(y), ptr(inp), ctypes.c_void_p(m), None, B)
+        return y
+
+    dense = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        xn = O.ref_rmsnorm(x, norms[0], 1e-6)
+        mm("q", xn), mm("k", xn), mm("v", xn)
+        x2 = x + mm("o", np.ascontiguousarray(xn))
+        xn = O.ref_rmsnorm(x2, norms[1], 1e-6)
+        g, u = mm("g", xn), mm("u", xn)
+        mid = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+        mm("d", mid)
+        dense.append(time.perf_counter() - t0)
+    attn = []
+    for i in range(len(kc)):
+        t0 = time.perf_counter()
+        _ref_attention(O, np.ascontiguousarray(q_rows[i:i + 1]), kc[i], vc[i], int(pos[i]), cores)
+        attn.append(time.perf_counter() - t0)
+    lm = R.ref_matrix_create(embed_bits.ctypes.data, 1, embed_bits.shape[0], embed_bits.shape[1])
+    y = np.empty((B, embed_bits.shape[0]), np.float32)
+    t0 = time.perf_counter()
+    R.ref_matrix_matmul(ptr(y), ptr(x), ctypes.c_void_p(lm), None, B)
+    t_lm = time.perf_counter() - t0
+    R.ref_matrix_destroy(ctypes.c_void_p(lm))
+    for m, _ in mats.values():
+        R.ref_matrix_destroy(ctypes.c_void_p(m))
+    t_layer = float(np.median(dense)) + float(np.mean(attn)) * B
+    t = layers * t_layer + t_lm
+    return {"value": round(B / t, 2), "unit": "tok/s", "cores": cores,
+            "kind": "reference" if O.ref_available() else "port",
+            "sample": f"one layer's dense ops for {B} rows (median of {reps}: "
+                      f"{float(np.median(dense)) * 1e3:.1f} ms), attention of {len(kc)} rows "
+                      f"(mean {float(np.mean(attn)) * 1e3:.2f} ms per row, x {B}), the LM head "
+                      f"once ({t_lm * 1e3:.0f} ms); step = {layers} layers + LM head",
+            "ms_per_step": round(t * 1e3, 1)}
+
+
 def cpu_baseline_mixed(O, pq_h, kc_pf, vc_pf, P, dq_h, dec_kv, budget_s=10.0):
     """Config 5 on the CPU: the reference's attention for the prompt's last rows (scaled
     to all 4,000 rows by their causal flop count) and for the 48 decode rows over
@@ -724,7 +784,7 @@ def bench_model(args, torch, ie, O):
     kv_bytes = decode_bytes(lens, KV_BYTES[kv])
     nbytes = layers * (w_bytes + kv_bytes) + wb * V * H + (4 * V if int8 else 0) + 4 * B * V
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {
+    res = {
         "metric": "decode step (24-layer Qwen2.5-0.5B shape, batch 64) tok/s, 1 GPU",
         "value": round(B / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
@@ -743,6 +803,24 @@ def bench_model(args, torch, ie, O):
         "bytes_note": "weights once per step, KV as config 3 per layer, the logits written; "
                       "activations (under 3%) not counted",
     }
+    if not args.no_cpu and not int8 and O.ref_available():
+        bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16).copy()
+        t0 = Wl[0]
+        layer_bits = {n: bits(t0[n]) for n in ("q", "k", "v", "o", "g", "u", "d")}
+        norms = [t0["inorm"].cpu().numpy(), t0["pnorm"].cpu().numpy()]
+        x_h = torch.randn((B, H), generator=gen, device=dev).cpu().numpy()
+        host = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+        kp0, vp0, tab0 = host(k_pools[0]), host(v_pools[0]), tabs[0].cpu().numpy()
+        kcs, vcs, ps = [], [], []
+        for r in range(8):  # a sample of rows, gathered to contiguous fp32
+            L = int(lens[r])
+            idx = tab0[r, np.arange(L) // PAGE].astype(np.int64) * PAGE + np.arange(L) % PAGE
+            kcs.append(O.widen_kv(kp0[idx], KV_CODES[kv]))
+            vcs.append(O.widen_kv(vp0[idx], KV_CODES[kv]))
+            ps.append(L - 1)
+        res["cpu_baseline"] = cpu_baseline_model(O, layer_bits, norms, bits(E), x_h, kcs, vcs,
+                                                 ps, layers)
+    return res
 
 
 def main():

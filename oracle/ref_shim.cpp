@@ -59,6 +59,20 @@ void ref_matmul_bf16(float* y, const float* x, const uint16_t* w_bits, int dtype
     for (size_t i = 0; i < m.i8.size(); ++i) i8_out[i] = m.i8[i];
 }
 
+// A matrix built once by ie::make_matrix_bf16 and then multiplied by
+// ie::matmul (AVX2 kernel, the reference's default) as often as a timing loop
+// needs: the CPU baseline of the decode step's projections.
+void* ref_matrix_create(const uint16_t* w_bits, int dtype, int rows, int cols) {
+  const ie::DType d = dtype == 0 ? ie::DType::F32 : dtype == 1 ? ie::DType::BF16 : ie::DType::I8;
+  return new ie::Matrix(ie::make_matrix_bf16(
+      std::vector<uint16_t>(w_bits, w_bits + size_t(rows) * cols), rows, cols, d));
+}
+void ref_matrix_destroy(void* m) { delete static_cast<ie::Matrix*>(m); }
+void ref_matrix_matmul(float* y, const float* x, const void* m, const float* bias, int T) {
+  ie::set_kernel(ie::Kernel::Avx2);
+  ie::matmul(y, x, *static_cast<const ie::Matrix*>(m), bias, T);
+}
+
 // ie::Matrix::row_to_f32 (src/matrix.cpp:60-67) of a bf16-bits matrix stored as `dtype`.
 void ref_row_to_f32(float* out, const uint16_t* w_bits, int dtype, int rows, int cols, int r) {
   const ie::DType d = dtype == 0 ? ie::DType::F32 : dtype == 1 ? ie::DType::BF16 : ie::DType::I8;
