@@ -34,9 +34,10 @@ constexpr int kMmWaves = 8;  // waves of a workgroup, splitting K
 
 using bf16 = __bf16;
 
-__device__ __forceinline__ bf16x8 load_weights(const void* w, bool int8, size_t idx) {
+template <bool I8>
+__device__ __forceinline__ bf16x8 load_weights(const void* w, size_t idx) {
   bf16x8 a;
-  if (!int8) {
+  if constexpr (!I8) {
     a = *reinterpret_cast<const bf16x8*>(static_cast<const uint16_t*>(w) + idx);
   } else {
     const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(w) + idx);
@@ -89,11 +90,11 @@ struct RowSplit {
   int split0, split1;
 };
 
-template <bool GATE, int RT, int TT, int W = kMmWaves>
+template <bool GATE, int RT, int TT, int W, bool I8>
 __global__ void __launch_bounds__(64 * W)
 matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const void* __restrict__ w,
                    const float* __restrict__ scale, const void* __restrict__ w2,
-                   const float* __restrict__ scale2, const float* __restrict__ bias, int int8,
+                   const float* __restrict__ scale2, const float* __restrict__ bias,
                    int T, int rows, int cols, int accumulate, RowSplit out) {
   constexpr int NA = GATE ? 2 : 1, NT = NA * RT * TT;
   static_assert(NT <= 16, "at most 16 accumulator tiles (64 KB of LDS for the reduction)");
@@ -120,8 +121,8 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
     bf16x8 a[NA][RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
-      a[0][i] = kin ? load_weights(w, int8, wrow[i] + k) : bf16x8{};
-      if constexpr (GATE) a[NA - 1][i] = kin ? load_weights(w2, int8, wrow[i] + k) : bf16x8{};
+      a[0][i] = kin ? load_weights<I8>(w, wrow[i] + k) : bf16x8{};
+      if constexpr (GATE) a[NA - 1][i] = kin ? load_weights<I8>(w2, wrow[i] + k) : bf16x8{};
     }
 #pragma unroll
     for (int j = 0; j < TT; ++j) {
@@ -170,7 +171,7 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
       for (int e = 0; e < 4; ++e) {
         const int row = row0 + 16 * i + 4 * g + e;
         if (row >= rows) break;
-        float v = acc[0][i][j][e] * (int8 ? scale[row] : 1.0f);
+        float v = acc[0][i][j][e] * (I8 ? scale[row] : 1.0f);
         float* dst;
         if (row < out.split0)
           dst = y + size_t(tok) * out.split0 + row;
@@ -179,7 +180,7 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
         else
           dst = out.y2 + size_t(tok) * (rows - out.split1) + (row - out.split1);
         if constexpr (GATE) {
-          v = silu(v) * (acc[NA - 1][i][j][e] * (int8 ? scale2[row] : 1.0f));
+          v = silu(v) * (acc[NA - 1][i][j][e] * (I8 ? scale2[row] : 1.0f));
         } else {
           if (bias) v += bias[row];
           if (accumulate) v += *dst;
@@ -272,14 +273,21 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   if (grid.y > 65535) return fail(IE_HIP_EINVAL, std::string(who) + ": too many tokens");
   const void* w2d = gate ? w2->data : nullptr;
   const float* s2 = gate ? w2->scale : nullptr;
-#define IE_MM_LAUNCH(G, R, C)                                                                    \
+#define IE_MM_LAUNCH_W(G, R, C, W)                                                               \
   do {                                                                                           \
-    if (R == 4)                                                                                  \
-      hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C, 4>), grid, block, 0, stream, y, x, w.data, \
-                         w.scale, w2d, s2, bias, w.int8, T, w.rows, w.cols, accumulate, split);  \
+    if (w.int8)                                                                                  \
+      hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C, W, true>), grid, block, 0, stream, y, x,   \
+                         w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols, accumulate, split);  \
     else                                                                                         \
-      hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C>), grid, block, 0, stream, y, x, w.data,    \
-                         w.scale, w2d, s2, bias, w.int8, T, w.rows, w.cols, accumulate, split);  \
+      hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C, W, false>), grid, block, 0, stream, y, x,  \
+                         w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols, accumulate, split);  \
+  } while (0)
+#define IE_MM_LAUNCH(G, R, C)          \
+  do {                                 \
+    if (R == 4)                        \
+      IE_MM_LAUNCH_W(G, R, C, 4);      \
+    else                               \
+      IE_MM_LAUNCH_W(G, R, C, kMmWaves); \
   } while (0)
 #define IE_MM_TT(G, R)            \
   if (TT == 4)                    \
@@ -303,6 +311,7 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   }
 #undef IE_MM_TT
 #undef IE_MM_LAUNCH
+#undef IE_MM_LAUNCH_W
   return check_launch(who);
 }
 
