@@ -198,15 +198,37 @@ rmsnorm_kernel(float* y, const float* x, const float* __restrict__ weight, int d
   __shared__ float part[4];
   const float* xt = x + size_t(blockIdx.x) * dim;
   float* yt = y + size_t(blockIdx.x) * dim;
+  // Rows up to 8 elements a thread (2,048 floats) stay in registers between
+  // the sum and the scaling, so the row is read once.
+  constexpr int kHeld = 8;
+  const bool held = dim <= kHeld * int(blockDim.x);
+  float xv[kHeld];
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += xt[i] * xt[i];
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+      const int i = int(threadIdx.x) + j * int(blockDim.x);
+      xv[j] = i < dim ? xt[i] : 0.0f;
+      ss += xv[j] * xv[j];
+    }
+  } else {
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) ss += xt[i] * xt[i];
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float total = (part[0] + part[1]) + (part[2] + part[3]);
   const float inv_rms = 1.0f / sqrtf(total / float(dim) + eps);
-  for (int i = threadIdx.x; i < dim; i += blockDim.x) yt[i] = xt[i] * inv_rms * weight[i];
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+      const int i = int(threadIdx.x) + j * int(blockDim.x);
+      if (i < dim) yt[i] = xv[j] * inv_rms * weight[i];
+    }
+  } else {
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) yt[i] = xt[i] * inv_rms * weight[i];
+  }
 }
 
 // x[t] = E[ids[t]] widened to f32 (times the row's scale for INT8).
