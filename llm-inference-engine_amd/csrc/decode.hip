@@ -219,16 +219,23 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
 }
 
 // Split-K merge: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M), M = max m_c.
+//
+// The order of the sums is fixed by the row alone, so a row's result does not
+// depend on the batch, the launch shape or the chunk count the caller sizes
+// the workspace for: the leaves are the row's chunks 0 .. nc-1 (nc from its
+// position and chunk_tokens); block b = chunks [8b, 8b+8) is folded in chunk
+// order, and the blocks are combined by a binary tree over b -- node (b, b+1),
+// then (b..b+1, b+2..b+3), ... each as merge(left, right). Slots past nc and
+// chunks that saw no position (m = -inf) are identities that every merge
+// passes through unchanged, so padding the tree to any width changes nothing.
+//
 // A workgroup takes one (head, row) and a slice of 64/S output dims (S = 1, 2
 // or 4 slices, more slices when rows x heads alone would leave compute units
-// idle). In a wave, lane = (chunk lane, dim quad): the slice's D/4 quads of
-// float4 side by side, and 64/(D/4) chunk lanes, so one load instruction
-// covers several chunks' slices. Chunk lane i of wave w takes the row's chunks
-// i + w*CL, i + (w + W)*CL, ..., kMergeBatch of them in flight at a time,
-// each folded into a running (M, L, acc) in natural-log units. The chunk
-// lanes are then combined by xor-shuffles and the waves through LDS with the
-// same rule: (M1, L1, A1) + (M2, L2, A2) = (M, L1 e^(M1-M) + L2 e^(M2-M), ...).
-constexpr int kMergeBatch = 8;
+// idle). In a wave, lane = (block lane, dim quad): the slice's Q quads of
+// float4 side by side and 64/Q block lanes; block lane i of wave w owns block
+// w * (64/Q) + i and loads its 8 chunks at once. The tree runs over lanes by
+// xor-shuffles, then over waves through LDS.
+constexpr int kMergeBlock = 8;
 constexpr int kMergeMaxWaves = 16;
 
 struct MergeAcc {
@@ -236,11 +243,14 @@ struct MergeAcc {
   float4 a;
 };
 
+// (M1, L1, A1) + (M2, L2, A2) = (M, L1 e^(M1-M) + L2 e^(M2-M), A1 e^(M1-M) +
+// A2 e^(M2-M)), M = max(M1, M2); an identity side (M = -inf) returns the
+// other side bit for bit.
 __device__ __forceinline__ MergeAcc merge_pair(const MergeAcc& x, const MergeAcc& y) {
+  if (y.m == -INFINITY) return x;
+  if (x.m == -INFINITY) return y;
   const float m = fmaxf(x.m, y.m);
-  if (m == -INFINITY) return x;  // neither side has seen a position
-  const float ex = x.m == -INFINITY ? 0.0f : expf(x.m - m);
-  const float ey = y.m == -INFINITY ? 0.0f : expf(y.m - m);
+  const float ex = expf(x.m - m), ey = expf(y.m - m);
   MergeAcc r;
   r.m = m;
   r.l = __builtin_fmaf(x.l, ex, y.l * ey);
@@ -272,7 +282,7 @@ decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
   __shared__ MergeAcc red[kMergeMaxWaves][Q];
   const int h = blockIdx.x, t = blockIdx.y, s = blockIdx.z;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
-  const int qd = lane % Q, cl = lane / Q;
+  const int qd = lane % Q, bl = lane / Q;
   const int p = row_pos[t];
   if (p < 0) return;
   const int nc = min(p / chunk_tokens + 1, num_chunks);
@@ -281,30 +291,26 @@ decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
   const int dim = s * 4 * Q + 4 * qd;
   const float2* ml = reinterpret_cast<const float2*>(part_ml) + base;
   const float4* po = reinterpret_cast<const float4*>(part_o + base * HD + dim);
+
+  // This lane's block, folded in chunk order.
+  const int b = w * CL + bl;
+  const int c0 = b * kMergeBlock;
+  float2 mlc[kMergeBlock];
+  float4 oc[kMergeBlock];
+#pragma unroll
+  for (int j = 0; j < kMergeBlock; ++j) {
+    const bool ok = c0 + j < nc;
+    mlc[j] = ok ? ml[c0 + j] : make_float2(-INFINITY, 0.0f);
+    oc[j] = ok ? po[size_t(c0 + j) * (HD / 4)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
   MergeAcc acc{-INFINITY, 0.0f, make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
-  const int stride = W * CL;
-  for (int c0 = w * CL + cl; c0 < nc; c0 += kMergeBatch * stride) {
-    float2 mlc[kMergeBatch];
-    float4 oc[kMergeBatch];
+  float mb = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
-      const int c = c0 + j * stride;
-      const bool ok = c < nc;
-      mlc[j] = ok ? ml[c] : make_float2(-INFINITY, 0.0f);
-      oc[j] = ok ? po[size_t(c) * (HD / 4)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-    float mb = acc.m;
+  for (int j = 0; j < kMergeBlock; ++j) mb = fmaxf(mb, mlc[j].x);
+  if (mb != -INFINITY) {
+    acc.m = mb;
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) mb = fmaxf(mb, mlc[j].x);
-    if (mb == -INFINITY) continue;  // no visible position yet
-    const float sc = acc.m == -INFINITY ? 0.0f : expf(acc.m - mb);
-    acc.l *= sc;
-    acc.a.x *= sc;
-    acc.a.y *= sc;
-    acc.a.z *= sc;
-    acc.a.w *= sc;
-#pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
+    for (int j = 0; j < kMergeBlock; ++j) {
       const float e = mlc[j].x == -INFINITY ? 0.0f : expf(mlc[j].x - mb);
       acc.l = __builtin_fmaf(mlc[j].y, e, acc.l);
       acc.a.x = __builtin_fmaf(oc[j].x, e, acc.a.x);
@@ -312,23 +318,28 @@ decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
       acc.a.z = __builtin_fmaf(oc[j].z, e, acc.a.z);
       acc.a.w = __builtin_fmaf(oc[j].w, e, acc.a.w);
     }
-    acc.m = mb;
   }
+  // Tree over the wave's blocks: at level `off`, the lane whose block index
+  // has that bit clear is the left child. Both children end up with the node.
 #pragma unroll
-  for (int off = Q; off < 64; off <<= 1) acc = merge_pair(acc, shfl_xor_acc(acc, off));
-  float4* dst = reinterpret_cast<float4*>(out + (size_t(t) * n_heads + h) * HD + dim);
-  if (W == 1) {
-    if (cl == 0) {
-      *dst = make_float4(acc.a.x / acc.l, acc.a.y / acc.l, acc.a.z / acc.l, acc.a.w / acc.l);
-    }
-    return;
+  for (int off = Q; off < 64; off <<= 1) {
+    const MergeAcc other = shfl_xor_acc(acc, off);
+    acc = (bl & (off / Q)) ? merge_pair(other, acc) : merge_pair(acc, other);
   }
-  if (cl == 0) red[w][qd] = acc;
-  __syncthreads();
-  if (w != 0 || cl != 0) return;
-  MergeAcc r = red[0][qd];
-  for (int i = 1; i < W; ++i) r = merge_pair(r, red[i][qd]);
-  *dst = make_float4(r.a.x / r.l, r.a.y / r.l, r.a.z / r.l, r.a.w / r.l);
+  float4* dst = reinterpret_cast<float4*>(out + (size_t(t) * n_heads + h) * HD + dim);
+  if (W > 1) {  // the tree continues over the waves, node (w, w + stride)
+    if (bl == 0) red[w][qd] = acc;
+    __syncthreads();
+    for (int stride = 1; stride < W; stride <<= 1) {
+      if (bl == 0 && (w & (2 * stride - 1)) == 0 && w + stride < W)
+        red[w][qd] = merge_pair(red[w][qd], red[w + stride][qd]);
+      __syncthreads();
+    }
+    if (w != 0) return;
+    acc = red[0][qd];
+  }
+  if (bl == 0)
+    *dst = make_float4(acc.a.x / acc.l, acc.a.y / acc.l, acc.a.z / acc.l, acc.a.w / acc.l);
 }
 
 template <int KV, int G>
@@ -378,29 +389,33 @@ int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T,
                  int num_chunks, int chunk_tokens, hipStream_t stream) {
   if (num_chunks <= 1) return IE_HIP_OK;
   // Dim slices: enough (head, row, slice) workgroups to reach every compute unit
-  // when rows x heads alone cannot (long-context batches of a few rows).
+  // when rows x heads alone cannot (long-context batches of a few rows), and
+  // enough block lanes for the longest row: a wave holds 4 x slices blocks of
+  // 8 chunks, a workgroup at most 16 waves. Neither choice changes the sums.
   const int64_t pairs = int64_t(T) * n_heads;
   const int cus = device_compute_units();
-  const int slices = pairs >= cus ? 1 : (2 * pairs >= cus ? 2 : 4);
-  const int quads = 16 / slices, chunk_lanes = 64 / quads;
-  // Waves: up to kMergeBatch chunks per lane in one pass over the longest row.
-  const int per_wave = chunk_lanes * kMergeBatch;
-  const int waves = std::min(kMergeMaxWaves, std::max(1, (num_chunks + per_wave - 1) / per_wave));
+  int slices = pairs >= cus ? 1 : (2 * pairs >= cus ? 2 : 4);
+  while (slices < 16 && int64_t(kMergeMaxWaves) * 4 * slices * kMergeBlock < num_chunks)
+    slices *= 2;
+  const int blocks_per_wave = 4 * slices;
+  const int blocks = (num_chunks + kMergeBlock - 1) / kMergeBlock;
+  const int waves = (blocks + blocks_per_wave - 1) / blocks_per_wave;
+  if (waves > kMergeMaxWaves)
+    return fail(IE_HIP_EINVAL, "attention: more than 8,192 chunks per row");
   const dim3 grid(n_heads, T, slices), block(64 * waves);
+#define IE_MERGE_CASE(S)                                                                     \
+  case S:                                                                                    \
+    hipLaunchKernelGGL((decode_merge_kernel<16 / S>), grid, block, 0, stream, out, ws.part_o, \
+                       ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);              \
+    break;
   switch (slices) {
-    case 1:
-      hipLaunchKernelGGL((decode_merge_kernel<16>), grid, block, 0, stream, out, ws.part_o,
-                         ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
-      break;
-    case 2:
-      hipLaunchKernelGGL((decode_merge_kernel<8>), grid, block, 0, stream, out, ws.part_o,
-                         ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
-      break;
-    default:
-      hipLaunchKernelGGL((decode_merge_kernel<4>), grid, block, 0, stream, out, ws.part_o,
-                         ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);
-      break;
+    IE_MERGE_CASE(1)
+    IE_MERGE_CASE(2)
+    IE_MERGE_CASE(4)
+    IE_MERGE_CASE(8)
+    IE_MERGE_CASE(16)
   }
+#undef IE_MERGE_CASE
   return check_launch("attention_merge");
 }
 
@@ -470,12 +485,9 @@ int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
   const int ctx = std::max(max_context, 1);
   if (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) {
     // Matrix-core kernel (measured on MI355X): 128-position chunks when that
-    // gives two workgroups per compute unit (one wave streams the chunk). With
-    // fewer rows, 128-position chunks still when 64-position ones would give two
-    // per unit: the kernel then splits each chunk over four waves of one page
-    // pair each, and the merge reads half the partials. 64 below that.
-    if (rows * ie_hip_attention_chunks(ctx, 128) >= 2 * cus) return 128;
-    return rows * ie_hip_attention_chunks(ctx, 64) >= 2 * cus ? 128 : 64;
+    // gives two workgroups per compute unit (one wave streams the chunk), 64
+    // below that.
+    return rows * ie_hip_attention_chunks(ctx, 128) >= 2 * cus ? 128 : 64;
   }
   // float32 (matrix-core kernel, one page in flight per wave; measured on
   // MI355X): the largest chunk up to 256 positions that still gives two

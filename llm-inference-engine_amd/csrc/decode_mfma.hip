@@ -28,8 +28,7 @@
 //
 // Layout of the work:
 //   One workgroup per non-empty (row, chunk) pair, with one wave per 128
-//   positions of the chunk, or per 32 when the grid is small
-//   (decode_mfma_waves); each wave streams its positions
+//   positions of the chunk (decode_mfma_waves); each wave streams its positions
 //   as page pairs (32 tokens, 2 pages), keeping the next pair's loads in flight
 //   while it computes the current one. The 1-D grid is numbered row by row over
 //   the chunks each row actually has (a prefix sum of the rows' chunk counts,
@@ -140,7 +139,9 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     return;  // past the batch's last chunk: the whole workgroup leaves
   const int s0 = c * chunk_tokens;
   const int n = min(s0 + chunk_tokens, p + 1) - s0;  // positions of this chunk
-  const bool single = s0 == 0 && p < chunk_tokens;  // the row fits this one chunk
+  // The row has one chunk (its context fits one, or the caller sized one):
+  // written here; the merge skips it, reading the same count.
+  const bool single = min(p / chunk_tokens + 1, num_chunks) == 1;
   const int waves = kOneWave ? 1 : blockDim.x >> 6;
   const int tw = chunk_tokens / waves;              // positions per wave (a multiple of 32)
   const int wt0 = wave * tw;                        // first position of this wave in the chunk
@@ -545,7 +546,9 @@ decode_partial_mfma_f32(float* __restrict__ out, float* __restrict__ part_o,
     return;  // past the batch's last chunk
   const int s0 = c * chunk_tokens;
   const int n = min(s0 + chunk_tokens, p + 1) - s0;  // positions of this chunk
-  const bool single = s0 == 0 && p < chunk_tokens;  // the row fits this one chunk
+  // The row has one chunk (its context fits one, or the caller sized one):
+  // written here; the merge skips it, reading the same count.
+  const bool single = min(p / chunk_tokens + 1, num_chunks) == 1;
   const int npg = (n + IE_HIP_PAGE_SIZE - 1) / IE_HIP_PAGE_SIZE;
   // Page ids of the chunk (at most 64 pages), one per lane, loaded once and read
   // per page with readlane (no table load waits inside the page loop), as in
@@ -702,16 +705,13 @@ bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_d
          chunk_tokens <= 1024;
 }
 
-// Waves per workgroup for a chunk. A wave streams its positions as page pairs,
-// one pair in flight while it computes the previous one, so a long stream per
-// wave hides latency when the grid is large; about one wave per 128 positions
-// then. When the grid gives fewer than two workgroups per compute unit, chunks
-// of four or more pairs take one wave per pair instead: every pair is in
-// flight at once. At most 8 waves, a whole number of pairs each.
-static int decode_mfma_waves(int chunk_tokens, int64_t slots) {
-  const bool small_grid = slots < 2 * int64_t(device_compute_units());
-  const int per_wave = small_grid && chunk_tokens >= 128 ? 32 : 128;
-  int w = std::max(1, std::min(kMaxWaves, chunk_tokens / per_wave));
+// Waves per workgroup for a chunk: one per 128 positions (at most 8, a whole
+// number of page pairs each). A wave streams its positions as page pairs, one
+// pair in flight while it computes the previous one. The split depends on the
+// chunk size alone, never on the grid: the waves' results are merged in a
+// fixed order, so a row's output is the same whatever batch it is in.
+static int decode_mfma_waves(int chunk_tokens) {
+  int w = std::max(1, std::min(kMaxWaves, chunk_tokens / 128));
   while (w > 1 && chunk_tokens % (32 * w) != 0) --w;
   return w;
 }
@@ -722,7 +722,7 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
                 hipStream_t stream, const FusedAppend* fused) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
   const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
-  const int waves = decode_mfma_waves(chunk_tokens, slots);
+  const int waves = decode_mfma_waves(chunk_tokens);
   const size_t lds = size_t(waves) * kTile;
   if (chunk_tokens / waves > 512)  // a wave's page ids live one per lane
     return fail(IE_HIP_EINVAL, "attention: more than 512 positions per wave");

@@ -274,23 +274,29 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
                           (w2 ? reinterpret_cast<uintptr_t>(w2->data) : 0);
   if (align & (w.int8 ? 7 : 15))
     return fail(IE_HIP_EINVAL, std::string(who) + ": x and the weights must be 16-byte aligned");
-  // Tiles per workgroup, from the count of 16 x 16 output tiles (measured on
-  // MI355X at 64 tokens): below 4 per compute unit (q/k/v/o and down at 896
-  // rows), one tile per workgroup keeps every unit busy; from 4 per unit
-  // (gate/up's 4,864 rows) two row tiles share each activation fragment;
-  // from 64 per unit (the 151,936-row LM head) 4 x 4 tiles read each weight
-  // once and each activation fragment a quarter as often. LM head at 64
-  // tokens: 366 -> 172 us; the others are slower with larger tiles.
+  // The waves of a workgroup split K, so their count fixes every output's
+  // summation order. It depends on the matrix alone, never on T: a token's
+  // result is then the same bit for bit whatever batch it is computed in (the
+  // reference's "batch of N == N single tokens" contract,
+  // src/cuda/cuda_runner.cu:798-829). Wide matrices (row tiles alone reach 16
+  // per compute unit: the 151,936-row LM head) take 4-wave workgroups of 4 x 4
+  // tiles: at ~140 registers a lane three fit on a compute unit where one of 8
+  // would (LM head at 64 tokens: 176 -> 149 us on MI355X), each weight is read
+  // once and each activation fragment a quarter as often (366 -> 172 us).
+  // Otherwise 8 waves, and the tiles per workgroup (which do not change the
+  // arithmetic) follow the count of 16 x 16 output tiles, measured at 64
+  // tokens: below 4 per compute unit (q/k/v/o and down at 896 rows) one tile
+  // per workgroup keeps every unit busy; from 4 per unit (gate/up's 4,864
+  // rows) two row tiles share each activation fragment.
   const int cus = device_compute_units();
+  const bool wide = (w.rows + 15) / 16 >= 16 * cus;
+  const int waves = wide ? 4 : kMmWaves;
   const int64_t tiles = int64_t((w.rows + 15) / 16) * ((T + 15) / 16);
-  const int RT = tiles >= 64 * int64_t(cus) ? 4 : tiles >= 4 * int64_t(cus) ? 2 : 1;
+  int RT = wide ? 4 : tiles >= 4 * int64_t(cus) ? 2 : 1;
+  if (gate) RT = std::min(RT, 2);  // two weight matrices: at most 2 row tiles
   const int tok_tiles = (T + 15) / 16;  // kernels exist for 1, 2 and 4 token tiles
-  const int TT = tiles < 64 * int64_t(cus) ? 1 : tok_tiles > 2 ? 4 : tok_tiles;
+  const int TT = !wide ? 1 : tok_tiles > 2 ? 4 : tok_tiles;
   const dim3 grid((w.rows + 16 * RT - 1) / (16 * RT), (T + 16 * TT - 1) / (16 * TT));
-  // 4 x 4 tiles hold ~140 registers a lane: in workgroups of 4 waves, three
-  // fit on a compute unit where one of 8 would (LM head at 64 tokens: 176 ->
-  // 149 us on MI355X).
-  const int waves = RT == 4 ? 4 : kMmWaves;
   const dim3 block(64 * waves);
   if (grid.y > 65535) return fail(IE_HIP_EINVAL, std::string(who) + ": too many tokens");
   const void* w2d = gate ? w2->data : nullptr;
@@ -304,11 +310,11 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
       hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C, W, false>), grid, block, 0, stream, y, x,  \
                          w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols, accumulate, split);  \
   } while (0)
-#define IE_MM_LAUNCH(G, R, C)          \
-  do {                                 \
-    if (R == 4)                        \
-      IE_MM_LAUNCH_W(G, R, C, 4);      \
-    else                               \
+#define IE_MM_LAUNCH(G, R, C)            \
+  do {                                   \
+    if (wide)                            \
+      IE_MM_LAUNCH_W(G, R, C, 4);        \
+    else                                 \
       IE_MM_LAUNCH_W(G, R, C, kMmWaves); \
   } while (0)
 #define IE_MM_TT(G, R)            \
@@ -318,8 +324,8 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
     IE_MM_LAUNCH(G, R, 2);        \
   else                            \
     IE_MM_LAUNCH(G, R, 1);
-  if (gate) {  // two weight matrices: at most 2 row tiles
-    if (RT >= 2) {
+  if (gate) {
+    if (RT == 2) {
       IE_MM_TT(true, 2)
     } else {
       IE_MM_TT(true, 1)

@@ -101,7 +101,7 @@ def test_chunk_helpers(ie):
     # helper assumes MI355X's 256 compute units.
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_F16) == 128
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_BF16) == 128
-    assert ie.attention_chunk_tokens(1, 32768, ie.KV_F16) == 128
+    assert ie.attention_chunk_tokens(1, 32768, ie.KV_F16) == 64
     assert ie.attention_chunk_tokens(1, 8192, ie.KV_BF16) == 64
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_F32) == 256
     assert ie.attention_chunk_tokens(1, 32768, ie.KV_F32) == 64

@@ -147,9 +147,12 @@ def test_chunk_size_invariance(ie, O, dev, impl):
 
 
 @pytest.mark.parametrize("kv", ["f16", "f32"])
-def test_config3_full_size(ie, O, dev, kv, impl):
+@pytest.mark.parametrize("partition", ["512", "bench"])
+def test_config3_full_size(ie, O, dev, kv, impl, partition):
     """batch 64, L ~ U[128, 4096], 16-token pages, tables a seeded
-    permutation of a 65,536-page pool, 512-token partitions."""
+    permutation of a 65,536-page pool; 512-token partitions (BASELINE's), and the
+    partition bench.py times (the library's own choice for 64 rows of up to 4,096
+    tokens, over the chunk count of the full 4,096)."""
     rng = np.random.default_rng(20263)
     kvt = KVS[kv]
     num_pages = 65536
@@ -169,9 +172,14 @@ def test_config3_full_size(ie, O, dev, kv, impl):
     q = normal(rng, (64, QD))
     want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
                              threads=8)
-    got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, 512,
-                        num_chunks=8)
-    check(O, got, want, kvt, "config 3")
+    if partition == "512":
+        ct, nc = 512, 8
+    else:
+        ct = ie.attention_chunk_tokens(64, 4096, kvt)
+        nc = ie.attention_chunks(4096, ct)
+    got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct,
+                        num_chunks=nc)
+    check(O, got, want, kvt, f"config 3, {ct}-token chunks")
 
 
 @pytest.mark.parametrize("rows", [1, 12, 24])

@@ -106,8 +106,10 @@ def test_matmul(ie, dev, case, int8):
 
 
 @pytest.mark.parametrize("int8", [False, True])
-@pytest.mark.parametrize("T", [1, 64])
+@pytest.mark.parametrize("T", [1, 64, 1024])
 def test_gate_up_silu(ie, dev, int8, T):
+    """T = 1,024 at 4,864 rows has more than 64 output tiles per compute unit: the launch
+    must still size its grid for the 2-row-tile gate kernel it runs."""
     rng = np.random.default_rng(7 + T)
     rows, cols = 4864, 896
     x = rng.standard_normal((T, cols), dtype=np.float32)

@@ -90,8 +90,8 @@ def test_matches_two_calls_and_oracle(ie, O, dev, kv, ct):
 
 @pytest.mark.parametrize("kv", list(KVS))
 def test_long_single_row(ie, O, dev, kv):
-    """One row at position 8,191: a small grid, so 128-token chunks run as four one-pair
-    waves per workgroup, and the appended position sits in the last wave's pair."""
+    """One row at position 8,191 in 512-token chunks: four waves per workgroup (128
+    positions each), and the appended position sits in the last wave's last pair."""
     kvt = KVS[kv]
     rng = np.random.default_rng(800 + kvt)
     L = 8192
@@ -100,7 +100,7 @@ def test_long_single_row(ie, O, dev, kv):
     row_pos, row_seq = np.array([L - 1], np.int32), np.zeros(1, np.int32)
     q, k, v = normal(rng, (1, QD)), normal(rng, (1, KVD)), normal(rng, (1, KVD))
     (fout, fkp, fvp, fq), (tout, tkp, tvp) = run_both(ie, dev, kvt, q, k, v, kp, vp, row_pos,
-                                                      row_seq, tables, max_pages, 128, L)
+                                                      row_seq, tables, max_pages, 512, L)
     assert np.array_equal(fq.view(np.uint32), q.view(np.uint32))
     assert np.array_equal(fkp, tkp) and np.array_equal(fvp, tvp)
     assert np.array_equal(fout.view(np.uint32), tout.view(np.uint32))

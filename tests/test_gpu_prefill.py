@@ -68,19 +68,32 @@ def test_prompts(ie, O, dev, case, kv, impl):
 
 
 @pytest.mark.parametrize("kv", ["f16", "bf16"])
-def test_config5_prefill_4000_into_churned_pool(ie, O, dev, kv, impl):
-    """BASELINE config 5 (prefill half): 25% of a pool's pages freed and re-allocated from a
-    seeded free list, then a 4,000-token chunk appended into fresh pages (RoPE+append kernel)
-    and attended causally. Pages are checked bit-exactly; attention on sampled rows."""
+def test_config5_mixed_step_into_churned_pool(ie, O, dev, kv, impl):
+    """BASELINE config 5, both halves of the step: 48 decode sequences (contexts
+    U[256, 2048]) hold pages; 12 of them (25%) finish and 12 new ones take their pages
+    back from the free list; then a 4,000-token prompt is appended into fresh pages
+    (RoPE+append kernel) and attended causally, and the 48 decode rows append their new
+    token and attend. Pages are checked bit-exactly; attention on every decode row and
+    on 256 sampled prompt rows plus the page and tile edges."""
     kvt = KVS[kv]
     rng = np.random.default_rng(20265)
     num_pages, T = 8192, 4000
     pool = ie.PagePool(num_pages, 64, 8192)
     seqs = [pool.open_sequence() for _ in range(48)]
+    lens = {}
     for s in seqs:
-        pool.ensure(s, int(rng.integers(256, 2049)))
-    for s in rng.permutation(seqs)[:12]:  # 25% of the decode sequences finish
-        pool.close_sequence(int(s))
+        lens[s] = int(rng.integers(256, 2049))
+        pool.ensure(s, lens[s])
+    done = [int(s) for s in rng.permutation(seqs)[:12]]  # 25% of the decode sequences finish
+    for s in done:
+        pool.close_sequence(s)
+        del lens[s]
+    for _ in done:  # ... and new ones re-allocate their pages from the free list
+        s = pool.open_sequence()
+        lens[s] = int(rng.integers(256, 2049))
+        pool.ensure(s, lens[s])
+    dec = sorted(lens)
+    assert len(dec) == 48
     p = pool.open_sequence()
     pool.ensure(p, T)
     max_pages = pool.max_pages_per_seq
@@ -106,10 +119,39 @@ def test_config5_prefill_4000_into_churned_pool(ie, O, dev, kv, impl):
     torch.cuda.synchronize()
     assert np.array_equal(from_dev(dq).view(np.uint32), q_rot.view(np.uint32))
     assert np.array_equal(from_dev(dkp), kp_ref) and np.array_equal(from_dev(dvp), vp_ref)
-    sample = np.unique(np.concatenate([[0, 1, 15, 16, 63, 64, T - 1], rng.integers(0, T, 25)]))
+    sample = np.unique(np.concatenate([[0, 1, 15, 16, 63, 64, 65, 127, 128, T - 2, T - 1],
+                                       rng.integers(0, T, 256)]))
     want = O.paged_attention(q_rot[sample], kp_ref, vp_ref, kvt, row_pos[sample], row_seq[sample],
                              tables, max_pages, NH, NKV, HD, threads=8)
     check(O, from_dev(out)[sample], want, kvt, "config 5 prefill")
+
+    # The decode half: each sequence's new token at its current length, appended and
+    # attended in one decode launch over the same (churned) pool.
+    for s in dec:
+        pool.ensure(s, lens[s] + 1)
+    tables = np.array(pool.host_tables(), np.int32).reshape(pool.max_batch, max_pages)
+    pool.upload_tables(dtab)
+    n = len(dec)
+    dpos_h = np.array([lens[s] for s in dec], np.int32)
+    dseq_h = np.array(dec, np.int32)
+    qd, kd, vd = normal(rng, (n, QD)), normal(rng, (n, KVD)), normal(rng, (n, KVD))
+    qd_rot, kp_ref, vp_ref = O.rope_append_paged(qd, kd, vd, kp_ref, vp_ref, kvt, dpos_h, dseq_h,
+                                                 tables, max_pages, NH, NKV, HD, THETA)
+    dqd = to_dev(qd, dev)
+    ddpos, ddseq = to_dev(dpos_h, dev), to_dev(dseq_h, dev)
+    ie.rope_and_cache(dqd, to_dev(kd, dev), to_dev(vd, dev), dkp, dvp, table, ddpos, ddseq, dtab,
+                      max_pages, NH, NKV, HD)
+    ct = ie.attention_chunk_tokens(n, 2049, kvt)
+    nc = ie.attention_chunks(2049, ct)
+    ws = ie.attention_workspace(n, NH, HD, nc)
+    dout = torch.full((n, QD), float("nan"), dtype=torch.float32, device=dev)
+    ie.attention(dout, dqd, dkp, dvp, ddpos, ddseq, dtab, max_pages, nc, ct, ws, NH, NKV, HD)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(dqd).view(np.uint32), qd_rot.view(np.uint32))
+    assert np.array_equal(from_dev(dkp), kp_ref) and np.array_equal(from_dev(dvp), vp_ref)
+    want = O.paged_attention(qd_rot, kp_ref, vp_ref, kvt, dpos_h, dseq_h, tables, max_pages, NH,
+                             NKV, HD, threads=8)
+    check(O, from_dev(dout), want, kvt, "config 5 decode rows")
 
 
 @pytest.mark.parametrize("kv", list(KVS))
