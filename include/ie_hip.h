@@ -233,6 +233,14 @@ int ie_hip_qkv_proj(float* q, float* k, float* v, const float* x, ie_matrix w_qk
 int ie_hip_gate_up_silu(float* out, const float* x, ie_matrix w_gate, ie_matrix w_up, int T,
                         hipStream_t stream);
 
+/* out[r] = index of the maximum of logits[r, 0..n) for r < R: the greedy
+ * token of each row, with the reference CPU argmax's semantics
+ * (src/sampler.cpp:26-31): the first strict maximum in index order (ties go
+ * to the lowest index), NaNs never chosen, 0 when element 0 is NaN or no
+ * element exceeds -inf. Replaces argmax_rows (src/cuda/kernels.cuh:106,
+ * kernels.cu:785-812), which returns INT_MAX for a row of -inf. */
+int ie_hip_argmax_rows(int32_t* out, const float* logits, int R, int n, hipStream_t stream);
+
 /* ------------------------------------------------------- page allocator ---
  * The page pool / free list / page tables behind BatchRunner (reference:
  * CudaEngine ctor src/cuda/cuda_runner.cu:191-204, open/close_sequence

@@ -129,6 +129,11 @@ inline void gather_rows(float* dst, const float* src, const int* rows, int R, in
   check(ie_hip_gather_rows(dst, src, rows, R, dim, stream));
 }
 
+/* argmax_rows (kernels.cuh:106): the greedy token of each logit row. */
+inline void argmax_rows(int32_t* out, const float* logits, int R, int n, hipStream_t stream) {
+  check(ie_hip_argmax_rows(out, logits, R, n, stream));
+}
+
 }  // namespace ie::hip
 
 #endif  // IE_HIP_HPP_

@@ -1,24 +1,36 @@
-/* The paged KV-cache half of the reference's CudaEngine
- * (src/cuda/cuda_runner.cu:133-622), in C++17 over the C ABI of libie_hip.so:
- *   - sequences and their pages (open_sequence, close_sequence, ensure_pages,
- *     the page table and its dirty upload), through ie_page_pool;
- *   - the per-layer pools, the RoPE table, the step's row buffers and the
- *     split-K workspace, sized before any graph is recorded (reserve);
- *   - one forward step over token rows (run): prompt detection, the chunk
- *     partition, and per layer RoPE + paged append then prefill or
- *     flash-decoding attention (enqueue), or both in one launch for a decode
- *     step of a 16-bit cache;
- *   - one HIP graph per decode batch size (capture_graph).
- * The model's own per-layer work (projections before attention, o_proj and the
- * MLP after it) is the caller's: a LayerBody whose two callbacks enqueue that
- * work on the engine's stream around each layer's attention. They write the
- * step's q, k, v rows (q(), k(), v()) and read attn(), and are recorded into
- * the decode graphs with everything else.
+/* The paged KV-cache engine over the C ABI of libie_hip.so (C++17, header-only;
+ * needs hip/hip_runtime_api.h and libamdhip64 for memory, streams and graphs).
+ * It is the paged-KV half of what the reference's CudaEngine does
+ * (src/cuda/cuda_runner.cu:133-622) -- sequences and their pages, one forward
+ * step over token rows, a graph per decode batch size -- built around one idea:
+ * every capacity is fixed at construction, so nothing is allocated, resized or
+ * re-recorded while serving.
  *
- * Header-only; needs hip/hip_runtime_api.h and libamdhip64 for memory, streams
- * and graphs. Not thread-safe: one thread owns an engine, as one engine thread
- * owns a BatchRunner in the reference (src/server.h:9-17). Every step is
- * synchronous on return (src/cuda/cuda_runner.cu:397-398). */
+ * Memory. One sizing pass lays out every device region the engine will ever use
+ * -- the per-layer K/V pools, the page table, the RoPE table, a step's input
+ * rows, its q/k/v/attention rows and the split-K workspace -- and one
+ * hipMalloc backs them all (DeviceArena); one pinned block stages a step's
+ * inputs. A HIP graph recorded for a batch size therefore stays valid for the
+ * engine's life.
+ *
+ * A step. run() takes rows (sequence, position, token id) and the rows whose
+ * logits are wanted. It takes pages for every row, classifies the step (a
+ * prompt -- 16+ consecutive positions of one sequence -- runs the prefill
+ * kernel; other steps run flash-decoding, with RoPE + append folded into the
+ * attention launch for a decode step of a 16-bit cache), packs the inputs into
+ * the staging block at offsets that depend only on the row counts, and sends
+ * them with ONE copy. A decode step replays its batch size's graph; any other
+ * step is enqueued directly. Per layer the model's LayerBody runs its work
+ * around the attention; its `begin` and `end` hooks run before the first layer
+ * and after the last (the embedding, the final norm and the LM head).
+ *
+ * Numerics do not depend on the batch: the flash-decoding partition
+ * (chunk_tokens) is fixed per engine from its capacity and KV type, and the
+ * kernels' reduction orders depend on that partition and each row alone.
+ *
+ * Not thread-safe: one thread owns an engine, as one engine thread owns a
+ * BatchRunner in the reference (src/server.h:9-17). run() only enqueues;
+ * sync() waits and surfaces kernel errors. */
 #ifndef IE_HIP_ENGINE_HPP_
 #define IE_HIP_ENGINE_HPP_
 
@@ -28,6 +40,7 @@
 #include <map>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "ie_hip.hpp"
@@ -45,77 +58,87 @@ struct KvConfig {
   int kv_dim() const { return num_kv_heads * head_dim; }
 };
 
-/* The model's work around layer `layer`'s attention for a step of `rows` rows,
- * enqueued on `stream` (kernels and device-to-device copies only: the body is
- * recorded into decode graphs). Either may be empty. */
-struct LayerBody {
-  std::function<void(int layer, int rows, hipStream_t stream)> before_attention;
-  std::function<void(int layer, int rows, hipStream_t stream)> after_attention;
+/* What an engine holds, fixed at construction. */
+struct EngineLimits {
+  int max_batch = 1;     // sequence slots; a decode step has at most this many rows
+  int max_seq_len = 0;   // tokens per sequence
+  int num_pages = 0;     // pages in each layer's pool
+  int step_rows = 0;     // rows one step holds (0: max(max_batch, min(max_seq_len, 4096)));
+                         // a longer prompt runs as several steps
+  int logit_rows = 0;    // rows one step may ask logits for (0: max(max_batch, 16))
 };
 
-/* How the last step ran (for callers' logs and the tests). */
+/* The model's work around the engine's attention for a step of `rows` rows,
+ * enqueued on `stream` (kernels and device copies only: recorded into the
+ * decode graphs). Any of them may be empty. */
+struct LayerBody {
+  std::function<void(int rows, hipStream_t stream)> begin;
+  std::function<void(int layer, int rows, hipStream_t stream)> before_attention;
+  std::function<void(int layer, int rows, hipStream_t stream)> after_attention;
+  std::function<void(int rows, int logit_rows, hipStream_t stream)> end;
+};
+
+/* How a step ran (for callers' logs and the tests). */
 struct StepInfo {
-  int rows = 0;
+  int rows = 0, logit_rows = 0;
   bool graph = false;   // replayed a decode graph
   bool prompt = false;  // prefill attention (rows: consecutive positions of one sequence)
   bool fused = false;   // RoPE + append + attention in one launch per layer
   int chunk_tokens = 0, chunks = 0;  // flash-decoding partition (0 for a prompt)
 };
 
-/* Device allocations owned by the engine, freed with it (DeviceMemory,
- * src/cuda/cuda_runner.cu:51-96). */
-class DeviceMemory {
+/* One allocation carved into aligned regions: sizes are added first (add()),
+ * then commit() makes the single hipMalloc and at() turns an offset into a
+ * pointer. Freed as a whole with the arena. */
+class DeviceArena {
  public:
-  DeviceMemory() = default;
-  DeviceMemory(const DeviceMemory&) = delete;
-  DeviceMemory& operator=(const DeviceMemory&) = delete;
-  ~DeviceMemory() {
-    for (void* p : ptrs_) (void)hipFree(p);
+  DeviceArena() = default;
+  DeviceArena(const DeviceArena&) = delete;
+  DeviceArena& operator=(const DeviceArena&) = delete;
+  ~DeviceArena() {
+    if (base_) (void)hipFree(base_);
   }
   template <class T>
-  T* alloc(size_t n) {
-    void* p = nullptr;
-    check(hipMalloc(&p, std::max<size_t>(n * sizeof(T), 256)), "hipMalloc");
-    ptrs_.push_back(p);
-    return static_cast<T*>(p);
+  size_t add(size_t count) {
+    const size_t off = (size_ + kAlign - 1) / kAlign * kAlign;
+    size_ = off + std::max<size_t>(count, 1) * sizeof(T);
+    return off;
   }
-  void release(void* p) {
-    auto it = std::find(ptrs_.begin(), ptrs_.end(), p);
-    if (it == ptrs_.end()) return;
-    (void)hipFree(p);
-    ptrs_.erase(it);
+  void commit(const char* what) {
+    if (base_) throw std::logic_error("DeviceArena: committed twice");
+    check(hipMalloc(reinterpret_cast<void**>(&base_), std::max<size_t>(size_, kAlign)), what);
   }
+  template <class T>
+  T* at(size_t off) const {
+    return reinterpret_cast<T*>(base_ + off);
+  }
+  size_t bytes() const { return size_; }
 
  private:
-  std::vector<void*> ptrs_;
+  static constexpr size_t kAlign = 256;
+  unsigned char* base_ = nullptr;
+  size_t size_ = 0;
 };
 
-/* Page-locked host staging that only grows (PinnedBuffer, src/cuda/cuda_runner.cu:100-122). */
-template <class T>
-class PinnedBuffer {
+/* Page-locked host memory of a fixed size, for the step's input copy. */
+class PinnedBlock {
  public:
-  PinnedBuffer() = default;
-  PinnedBuffer(const PinnedBuffer&) = delete;
-  PinnedBuffer& operator=(const PinnedBuffer&) = delete;
-  ~PinnedBuffer() { reset(); }
-  void resize(size_t n) {
-    if (n <= n_) return;
-    reset();
-    void* p = nullptr;
-    check(hipHostMalloc(&p, n * sizeof(T), hipHostMallocDefault), "hipHostMalloc");
-    p_ = static_cast<T*>(p);
-    n_ = n;
+  PinnedBlock() = default;
+  PinnedBlock(const PinnedBlock&) = delete;
+  PinnedBlock& operator=(const PinnedBlock&) = delete;
+  ~PinnedBlock() {
+    if (p_) (void)hipHostFree(p_);
   }
-  T* data() { return p_; }
+  void allocate(size_t bytes, const char* what) {
+    check(hipHostMalloc(&p_, std::max<size_t>(bytes, 64), hipHostMallocDefault), what);
+  }
+  template <class T>
+  T* as() const {
+    return static_cast<T*>(p_);
+  }
 
  private:
-  void reset() {
-    if (p_) (void)hipHostFree(p_);
-    p_ = nullptr;
-    n_ = 0;
-  }
-  T* p_ = nullptr;
-  size_t n_ = 0;
+  void* p_ = nullptr;
 };
 
 class KvEngine {
@@ -124,7 +147,7 @@ class KvEngine {
    * src/cuda/cuda_runner.cu:38). */
   static constexpr int kPromptMinRows = 16;
 
-  /* Pages for a KV byte budget: as many as fit, but never more than every
+  /* Pages for a KV byte budget: as many as fit, never more than every
    * sequence at full length (make_batch_runner, src/cuda/cuda_runner.cu:612-622). */
   static int pages_for_budget(const KvConfig& cfg, int max_batch, int max_seq_len,
                               size_t kv_bytes, int kv_dtype) {
@@ -135,39 +158,74 @@ class KvEngine {
     return int(std::min(want, most));
   }
 
-  /* The constructor of src/cuda/cuda_runner.cu:146-204, less the weights:
-   * pools for every layer, the page table, the RoPE table (built on the host,
-   * so page writes match the CPU path bit for bit) and the stream. */
-  KvEngine(const KvConfig& cfg, int max_batch, int max_seq_len, int num_pages, bool use_graphs,
-           int kv_dtype, LayerBody body = {})
-      : cfg_(cfg), max_batch_(max_batch), max_seq_len_(max_seq_len), num_pages_(num_pages),
-        use_graphs_(use_graphs), kv_dtype_(kv_dtype), body_(std::move(body)) {
+  KvEngine(const KvConfig& cfg, const EngineLimits& limits, int kv_dtype, bool use_graphs,
+           LayerBody body = {})
+      : cfg_(cfg), lim_(limits), kv_dtype_(kv_dtype), use_graphs_(use_graphs),
+        body_(std::move(body)) {
     if (kv_dtype != IE_KV_F32 && kv_dtype != IE_KV_F16 && kv_dtype != IE_KV_BF16)
       throw std::runtime_error("KV cache: dtype must be IE_KV_F32, IE_KV_F16 or IE_KV_BF16");
     if (cfg.num_layers < 1 || cfg.num_heads < 1 || cfg.num_kv_heads < 1 || cfg.head_dim < 2)
       throw std::runtime_error("KV cache: bad model shape");
-    pages_ = ie_pages_create(num_pages, max_batch, max_seq_len);
+    if (lim_.max_batch < 1 || lim_.max_seq_len < 1) throw std::runtime_error("KV cache: bad limits");
+    if (lim_.num_pages < 1) throw std::runtime_error("KV cache: no pages");
+    if (lim_.step_rows <= 0) lim_.step_rows = std::max(lim_.max_batch, std::min(lim_.max_seq_len, 4096));
+    if (lim_.logit_rows <= 0) lim_.logit_rows = std::max(lim_.max_batch, kPromptMinRows);
+    lim_.step_rows = std::max(lim_.step_rows, lim_.max_batch);
+    lim_.logit_rows = std::max(lim_.logit_rows, lim_.max_batch);
+
+    // The flash-decoding partition, fixed for the engine's life: sized for a
+    // full batch of the longest sequences, so a step's numerics never depend on
+    // which rows it carries.
+    chunk_tokens_ = attention_chunk_tokens(lim_.max_batch, lim_.max_seq_len, kv_dtype_);
+    max_chunks_ = attention_chunks(lim_.max_seq_len, chunk_tokens_);
+    attn_rows_ = std::max(lim_.max_batch, kPromptMinRows);  // rows per flash-decoding launch
+
+    pages_ = ie_pages_create(lim_.num_pages, lim_.max_batch, lim_.max_seq_len);
     if (!pages_) throw std::runtime_error(ie_hip_last_error());
     try {
       max_pages_per_seq_ = ie_pages_max_pages_per_seq(pages_);
       hipDeviceProp_t prop{};
       check(hipGetDeviceProperties(&prop, 0), "hipGetDeviceProperties");
-      static const char* const kNames[] = {"", ", f16 KV cache", ", bf16 KV cache"};
+      static const char* const kKv[] = {"", ", f16 KV cache", ", bf16 KV cache"};
       name_ = std::string("hip, ") + prop.name + " (" + prop.gcnArchName + ")" +
-              (use_graphs_ ? ", graphs" : ", no graphs") + kNames[kv_dtype];
+              (use_graphs_ ? ", graphs" : ", no graphs") + kKv[kv_dtype];
       check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+      check(hipEventCreateWithFlags(&staged_, hipEventDisableTiming), "hipEventCreate");
 
-      std::vector<float> table(size_t(max_seq_len) * cfg.head_dim);
-      check(ie_hip_rope_table(table.data(), max_seq_len, cfg.head_dim, cfg.rope_theta));
-      rope_table_ = mem_.alloc<float>(table.size());
-      check(hipMemcpy(rope_table_, table.data(), table.size() * sizeof(float),
-                      hipMemcpyHostToDevice),
-            "rope table");
+      // Layout: pools, table, RoPE table, step inputs, step rows, workspace.
+      const int R = lim_.step_rows;
+      layer_bytes_ = size_t(lim_.num_pages) * kPageSize * cfg.kv_dim() * kv_elem_bytes(kv_dtype);
+      const size_t o_pools = arena_.add<unsigned char>(2 * layer_bytes_ * cfg.num_layers);
+      const size_t o_tables = arena_.add<int32_t>(size_t(lim_.max_batch) * max_pages_per_seq_);
+      const size_t o_rope = arena_.add<float>(size_t(lim_.max_seq_len) * cfg.head_dim);
+      const size_t o_in = arena_.add<int32_t>(input_ints());
+      const size_t o_q = arena_.add<float>(size_t(R) * cfg.q_dim());
+      const size_t o_k = arena_.add<float>(size_t(R) * cfg.kv_dim());
+      const size_t o_v = arena_.add<float>(size_t(R) * cfg.kv_dim());
+      const size_t o_attn = arena_.add<float>(size_t(R) * cfg.q_dim());
+      const size_t o_ws = arena_.add<unsigned char>(
+          attention_workspace_bytes(attn_rows_, cfg.num_heads, cfg.head_dim, max_chunks_));
+      arena_.commit("hipMalloc(KV engine)");
+      pools_ = arena_.at<unsigned char>(o_pools);
+      tables_ = arena_.at<int32_t>(o_tables);
+      rope_ = arena_.at<float>(o_rope);
+      inputs_ = arena_.at<int32_t>(o_in);
+      q_ = arena_.at<float>(o_q);
+      k_ = arena_.at<float>(o_k);
+      v_ = arena_.at<float>(o_v);
+      attn_ = arena_.at<float>(o_attn);
+      workspace_ = arena_.at<unsigned char>(o_ws);
+      staging_.allocate(input_ints() * sizeof(int32_t), "hipHostMalloc(step inputs)");
 
-      layer_bytes_ = size_t(num_pages_) * kPageSize * cfg.kv_dim() * kv_elem_bytes(kv_dtype);
-      k_pool_ = mem_.alloc<unsigned char>(layer_bytes_ * cfg.num_layers);
-      v_pool_ = mem_.alloc<unsigned char>(layer_bytes_ * cfg.num_layers);
-      tables_ = mem_.alloc<int32_t>(size_t(max_batch) * max_pages_per_seq_);
+      // The RoPE table, built on the host with libm exactly as the reference's
+      // CPU rope computes its angles, so page writes match it bit for bit.
+      std::vector<float> table(size_t(lim_.max_seq_len) * cfg.head_dim);
+      check(ie_hip_rope_table(table.data(), lim_.max_seq_len, cfg.head_dim, cfg.rope_theta));
+      check(hipMemcpy(rope_, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice),
+            "RoPE table");
+      // The device table starts as the host one does (zero-filled).
+      check(ie_pages_upload_tables(pages_, tables_, stream_, nullptr));
+      check(hipStreamSynchronize(stream_), "KV engine setup");
     } catch (...) {
       release();
       throw;
@@ -177,72 +235,156 @@ class KvEngine {
   KvEngine& operator=(const KvEngine&) = delete;
   ~KvEngine() { release(); }
 
-  // ----------------------------------------- BatchRunner (src/runner.h:52-80)
+  // ---------------------------------------------- sequences and the pool
 
   int open_sequence() { return ie_pages_open_sequence(pages_); }
   void close_sequence(int seq) { check(ie_pages_close_sequence(pages_, seq)); }
-  /* Tokens cached for seq: 0 for a closed slot, std::out_of_range past the
-   * slots (seqs_.at(seq).len, src/cuda/cuda_runner.cu:254). */
+  /* Tokens cached for seq: 0 for a closed slot, std::out_of_range past the slots
+   * (the reference reads seqs_.at(seq).len, src/cuda/cuda_runner.cu:254). */
   int sequence_length(int seq) const {
-    if (seq < 0 || seq >= max_batch_) throw std::out_of_range("sequence id " + std::to_string(seq));
+    if (seq < 0 || seq >= lim_.max_batch) throw std::out_of_range("sequence id " + std::to_string(seq));
     return std::max(ie_pages_sequence_length(pages_, seq), 0);
   }
-  int max_batch() const { return max_batch_; }
-  int max_seq_len() const { return max_seq_len_; }
+  bool is_open(int seq) const { return ie_pages_sequence_length(pages_, seq) >= 0; }
+  int max_batch() const { return lim_.max_batch; }
+  int max_seq_len() const { return lim_.max_seq_len; }
   int page_size() const { return kPageSize; }
   int total_pages() const { return ie_pages_total_pages(pages_); }
   int free_pages() const { return ie_pages_free_pages(pages_); }
   const KvConfig& config() const { return cfg_; }
+  const EngineLimits& limits() const { return lim_; }
   std::string device_name() const { return name_; }
   size_t kv_cache_bytes() const { return 2 * layer_bytes_ * size_t(cfg_.num_layers); }
 
-  /* Appends T prompt rows to seq (run_prefill, src/cuda/cuda_runner.cu:315-323):
-   * one row replays the batch-1 decode graph; 16 or more run the prefill
-   * attention kernel. */
+  // ----------------------------------------------------------- a step
+
+  /* Queues one forward step over rows (seq[t], pos[t]) with token ids ids[t]
+   * (may be empty when the LayerBody reads none) and logits wanted for rows
+   * `logit_rows` (indices into the step's rows). `decode`: one row per
+   * sequence, which may replay this batch size's graph. `after_layer` (direct
+   * steps only) runs on the host after each layer's work is queued, and with
+   * layer -1 after the body's `begin` (the embedding). Returns
+   * without waiting; sync() waits. Each listed sequence's length becomes its
+   * highest row position + 1 if that is longer. */
+  StepInfo run(const std::vector<int>& seq, const std::vector<int>& pos,
+               const std::vector<int32_t>& ids, const std::vector<int>& logit_rows, bool decode,
+               const std::function<void(int layer)>& after_layer = nullptr) {
+    const int T = int(seq.size()), R = int(logit_rows.size());
+    if (T == 0) throw std::runtime_error("forward: no tokens");
+    if (int(pos.size()) != T) throw std::runtime_error("forward: one position per row");
+    if (!ids.empty() && int(ids.size()) != T) throw std::runtime_error("forward: one token per row");
+    if (T > lim_.step_rows)
+      throw std::runtime_error("forward: " + std::to_string(T) + " rows in one step (at most " +
+                               std::to_string(lim_.step_rows) + ")");
+    if (R > lim_.logit_rows) throw std::runtime_error("forward: too many logit rows in one step");
+    for (int r : logit_rows)
+      if (r < 0 || r >= T) throw std::runtime_error("forward: logit row out of range");
+    int max_pos = 0;
+    for (int t = 0; t < T; ++t) {
+      if (pos[t] < 0) throw std::runtime_error("forward: negative position");
+      if (!is_open(seq[t]))
+        throw std::runtime_error("invalid or closed sequence id " + std::to_string(seq[t]));
+      check(ie_pages_ensure(pages_, seq[t], pos[t] + 1));
+      max_pos = std::max(max_pos, pos[t]);
+    }
+    const bool distinct = distinct_sequences(seq);
+    if (decode && !distinct) throw std::runtime_error("decode: one row per sequence");
+
+    StepInfo s;
+    s.rows = T;
+    s.logit_rows = R;
+    s.graph = decode && use_graphs_ && !after_layer && T <= lim_.max_batch;
+    s.prompt = !decode && T >= kPromptMinRows &&
+               attention_prefill_supported(cfg_.num_heads, cfg_.num_kv_heads, cfg_.head_dim);
+    for (int t = 1; s.prompt && t < T; ++t)
+      s.prompt = seq[t] == seq[0] && pos[t] == pos[0] + t;
+    if (!s.prompt) {
+      s.chunk_tokens = chunk_tokens_;
+      // A recorded graph covers any position a sequence can reach; a direct
+      // step only the context it has (the count does not change the sums).
+      s.chunks = s.graph ? max_chunks_ : attention_chunks(max_pos + 1, chunk_tokens_);
+      s.fused = distinct && rope_cache_attention_supported(kv_dtype_, cfg_.num_heads,
+                                                           cfg_.num_kv_heads, cfg_.head_dim,
+                                                           chunk_tokens_);
+    }
+
+    // Inputs: [seq T][pos T][ids T][logit rows R], one copy. The offsets depend
+    // only on T, so a decode graph (one per T and R) reads them where it recorded.
+    check(hipEventSynchronize(staged_), "staging");  // the previous step's copy is done
+    int32_t* h = staging_.as<int32_t>();
+    std::copy(seq.begin(), seq.end(), h);
+    std::copy(pos.begin(), pos.end(), h + T);
+    if (ids.empty())
+      std::fill(h + 2 * T, h + 3 * T, 0);
+    else
+      std::copy(ids.begin(), ids.end(), h + 2 * T);
+    std::copy(logit_rows.begin(), logit_rows.end(), h + 3 * T);
+    check(hipMemcpyAsync(inputs_, h, sizeof(int32_t) * (3 * size_t(T) + R), hipMemcpyHostToDevice,
+                         stream_),
+          "step inputs");
+    check(hipEventRecord(staged_, stream_), "hipEventRecord");
+    check(ie_pages_upload_tables(pages_, tables_, stream_, nullptr));  // only after page changes
+
+    cur_rows_ = T;
+    cur_logit_rows_ = R;
+    if (s.graph) {
+      auto it = graphs_.find({T, R});
+      if (it == graphs_.end()) it = graphs_.emplace(std::make_pair(T, R), record(s)).first;
+      check(hipGraphLaunch(it->second, stream_), "hipGraphLaunch");
+    } else {
+      enqueue(s, after_layer);
+    }
+    for (int t = 0; t < T; ++t)
+      if (pos[t] + 1 > ie_pages_sequence_length(pages_, seq[t]))
+        check(ie_pages_set_sequence_length(pages_, seq[t], pos[t] + 1));
+    last_ = s;
+    return s;
+  }
+
+  /* Waits for the queued work; kernel faults surface here (the reference's
+   * per-step synchronize, src/cuda/cuda_runner.cu:397-398). */
+  void sync() { check(hipStreamSynchronize(stream_), "forward"); }
+
+  // Steps without a model (the tests drive attention with their own q/k/v):
+
+  /* T prompt rows appended to seq; one row replays the batch-1 decode graph. */
   void prefill(int seq, int T) {
     if (T <= 0) throw std::runtime_error("forward: no tokens");
     const int start = checked_length(seq);
-    std::vector<int> rows_seq(T, seq), rows_pos(T);
-    for (int i = 0; i < T; ++i) rows_pos[i] = start + i;
-    run(rows_seq, rows_pos, /*graph=*/T == 1);
-    check(ie_pages_set_sequence_length(pages_, seq, start + T));
+    std::vector<int> rs(T, seq), rp(T);
+    for (int i = 0; i < T; ++i) rp[i] = start + i;
+    run(rs, rp, {}, {}, /*decode=*/T == 1);
+    sync();
   }
-
-  /* One new row for each listed sequence, replaying the decode graph of that
-   * batch size (run_decode, src/cuda/cuda_runner.cu:325-337). */
+  /* One new row for each listed sequence (a decode step). */
   void decode(const std::vector<int>& seqs) {
-    std::vector<int> rows_pos(seqs.size());
-    for (size_t i = 0; i < seqs.size(); ++i) rows_pos[i] = checked_length(seqs[i]);
-    run(seqs, rows_pos, /*graph=*/true);
-    for (size_t i = 0; i < seqs.size(); ++i)
-      check(ie_pages_set_sequence_length(pages_, seqs[i], rows_pos[i] + 1));
+    std::vector<int> rp(seqs.size());
+    for (size_t i = 0; i < seqs.size(); ++i) rp[i] = checked_length(seqs[i]);
+    run(seqs, rp, {}, {}, /*decode=*/true);
+    sync();
+  }
+  /* Any mix of rows in one direct step. */
+  void forward(const std::vector<int>& seq, const std::vector<int>& pos) {
+    run(seq, pos, {}, {}, /*decode=*/false);
+    sync();
   }
 
-  /* Any mix of rows (prompt chunks and decodes of several sequences) in one
-   * direct step; each sequence's length becomes its highest row position + 1
-   * if that is longer. */
-  void forward(const std::vector<int>& rows_seq, const std::vector<int>& rows_pos) {
-    run(rows_seq, rows_pos, /*graph=*/false);
-    for (size_t t = 0; t < rows_seq.size(); ++t)
-      if (rows_pos[t] + 1 > ie_pages_sequence_length(pages_, rows_seq[t]))
-        check(ie_pages_set_sequence_length(pages_, rows_seq[t], rows_pos[t] + 1));
-  }
+  // ------------------------------ the current step's buffers (for the body)
 
-  // ------------------------------------------ the step's device buffers
-
-  float* q() { return q_; }        // [rows, q_dim]: the layer's queries (RoPE in place, or not read back)
+  int32_t* ids() { return inputs_ + 2 * size_t(cur_rows_); }         // [rows]
+  int32_t* logit_row_ids() { return inputs_ + 3 * size_t(cur_rows_); }  // [logit rows]
+  float* q() { return q_; }        // [rows, q_dim]: the layer's queries
   float* k() { return k_; }        // [rows, kv_dim]: the layer's new keys
   float* v() { return v_; }        // [rows, kv_dim]: the layer's new values
   float* attn() { return attn_; }  // [rows, q_dim]: the layer's attention output
   hipStream_t stream() const { return stream_; }
-  int row_capacity() const { return cap_rows_; }
 
-  // --------------------------------------------------------- inspection
+  // ------------------------------------------------------- inspection
 
   const StepInfo& last_step() const { return last_; }
   int decode_graphs() const { return int(graphs_.size()); }
-  /* Replaces the model's per-layer work (for a body that needs the engine
-   * itself, as DecoderModel's does); recorded decode graphs are dropped. */
+  int chunk_tokens() const { return chunk_tokens_; }
+  /* Replaces the model's per-layer work; graphs recorded with the old one go. */
   void set_body(LayerBody body) {
     body_ = std::move(body);
     drop_graphs();
@@ -251,79 +393,23 @@ class KvEngine {
   const int32_t* host_tables() const { return ie_pages_host_tables(pages_); }
   const int32_t* device_tables() const { return tables_; }
   size_t layer_pool_bytes() const { return layer_bytes_; }
-  void* k_pool(int layer) { return k_pool_ + size_t(layer) * layer_bytes_; }
-  void* v_pool(int layer) { return v_pool_ + size_t(layer) * layer_bytes_; }
+  void* k_pool(int layer) { return pools_ + size_t(2 * layer) * layer_bytes_; }
+  void* v_pool(int layer) { return pools_ + size_t(2 * layer + 1) * layer_bytes_; }
   int kv_dtype() const { return kv_dtype_; }
+  size_t device_bytes() const { return arena_.bytes(); }
   int sequence_pages(int seq, int32_t* out, int cap) const {
     return ie_pages_sequence_pages(pages_, seq, out, cap);
   }
 
-  /* One forward step over rows (rows_seq[t], rows_pos[t]) -- the path part of
-   * CudaEngine::run (src/cuda/cuda_runner.cu:342-399): pages for every row,
-   * prompt detection, the chunk partition, scratch sized before any capture,
-   * the row and table uploads, then the decode graph or a direct enqueue, and
-   * a synchronize that surfaces kernel errors. `graph`: a pure decode step (one
-   * row per sequence) that may replay a recording. Sequence lengths are left
-   * to the caller (prefill/decode/forward advance them). */
-  void run(const std::vector<int>& rows_seq, const std::vector<int>& rows_pos, bool graph) {
-    const int T = int(rows_seq.size());
-    if (T == 0) throw std::runtime_error("forward: no tokens");
-    if (int(rows_pos.size()) != T) throw std::runtime_error("forward: one position per row");
-    int max_pos = 0;
-    for (int t = 0; t < T; ++t) {
-      if (rows_pos[t] < 0) throw std::runtime_error("forward: negative position");
-      check(ie_pages_ensure(pages_, rows_seq[t], rows_pos[t] + 1));
-      max_pos = std::max(max_pos, rows_pos[t]);
-    }
-    graph = graph && use_graphs_;
-    std::vector<int> sorted(rows_seq);
-    std::sort(sorted.begin(), sorted.end());
-    const bool distinct = std::adjacent_find(sorted.begin(), sorted.end()) == sorted.end();
-    if (graph && !distinct) throw std::runtime_error("decode: one row per sequence");
+ private:
+  size_t input_ints() const { return 3 * size_t(lim_.step_rows) + size_t(lim_.logit_rows); }
 
-    // A prompt (16+ consecutive positions of one sequence) runs the prefill
-    // kernel; the choice depends only on the rows themselves.
-    bool prompt = !graph && T >= kPromptMinRows &&
-                  attention_prefill_supported(cfg_.num_heads, cfg_.num_kv_heads, cfg_.head_dim);
-    for (int t = 1; prompt && t < T; ++t)
-      prompt = rows_seq[t] == rows_seq[0] && rows_pos[t] == rows_pos[0] + t;
-
-    StepInfo s;
-    s.rows = T;
-    s.graph = graph;
-    s.prompt = prompt;
-    if (!prompt) {
-      // A recorded graph covers every position a sequence can reach; a direct
-      // launch only the context it has.
-      const int ctx = graph ? max_seq_len_ : max_pos + 1;
-      s.chunk_tokens = attention_chunk_tokens(T, ctx, kv_dtype_);
-      s.chunks = attention_chunks(ctx, s.chunk_tokens);
-      s.fused = distinct && rope_cache_attention_supported(kv_dtype_, cfg_.num_heads,
-                                                           cfg_.num_kv_heads, cfg_.head_dim,
-                                                           s.chunk_tokens);
-    }
-    reserve(T, s.chunks);  // before any capture: no allocation may happen inside a graph
-    if (graph && !graphs_.count(T)) capture_graph(s);
-
-    std::memcpy(h_row_seq_.data(), rows_seq.data(), sizeof(int) * T);
-    std::memcpy(h_row_pos_.data(), rows_pos.data(), sizeof(int) * T);
-    check(hipMemcpyAsync(row_seq_, h_row_seq_.data(), sizeof(int) * T, hipMemcpyHostToDevice,
-                         stream_),
-          "row_seq");
-    check(hipMemcpyAsync(row_pos_, h_row_pos_.data(), sizeof(int) * T, hipMemcpyHostToDevice,
-                         stream_),
-          "row_pos");
-    check(ie_pages_upload_tables(pages_, tables_, stream_, nullptr));  // only if a page changed
-
-    if (graph)
-      check(hipGraphLaunch(graphs_.at(T), stream_), "hipGraphLaunch");
-    else
-      enqueue(s);
-    check(hipStreamSynchronize(stream_), "forward");
-    last_ = s;
+  static bool distinct_sequences(const std::vector<int>& seq) {
+    std::vector<int> s(seq);
+    std::sort(s.begin(), s.end());
+    return std::adjacent_find(s.begin(), s.end()) == s.end();
   }
 
- private:
   int checked_length(int seq) const {
     const int len = ie_pages_sequence_length(pages_, seq);
     if (len < 0) throw std::runtime_error("invalid or closed sequence id " + std::to_string(seq));
@@ -336,43 +422,59 @@ class KvEngine {
     kv.max_pages = max_pages_per_seq_;
     kv.page_size = kPageSize;
     kv.kv_dtype = kv_dtype_;
-    kv.num_pages = num_pages_;
+    kv.num_pages = lim_.num_pages;
     return kv;
   }
 
-  /* Every layer of a step on stream_ (the attention block of
-   * src/cuda/cuda_runner.cu:418-446, around the caller's LayerBody). */
-  void enqueue(const StepInfo& s) {
+  /* Every layer of a step on stream_ (the reference's per-layer order,
+   * src/cuda/cuda_runner.cu:418-446, with the model's work in the body).
+   * Flash-decoding runs in launches of at most attn_rows_ rows, the rows the
+   * workspace holds; a prompt runs the prefill kernel over all its rows. */
+  void enqueue(const StepInfo& s, const std::function<void(int)>& after_layer) {
     const int T = s.rows, NH = cfg_.num_heads, NKV = cfg_.num_kv_heads, HD = cfg_.head_dim;
     const KvLayout kv = layout();
+    const int32_t* rseq = inputs_;
+    const int32_t* rpos = inputs_ + T;
+    if (body_.begin) body_.begin(T, stream_);
+    if (after_layer) after_layer(-1);
     for (int l = 0; l < cfg_.num_layers; ++l) {
       if (body_.before_attention) body_.before_attention(l, T, stream_);
       void* kp = k_pool(l);
       void* vp = v_pool(l);
       if (s.fused) {
-        rope_cache_attention(attn_, q_, k_, v_, kp, vp, rope_table_, max_seq_len_, T, row_pos_,
-                             row_seq_, kv, s.chunks, s.chunk_tokens, workspace_, NH, NKV, HD,
-                             stream_);
+        for (int r0 = 0; r0 < T; r0 += attn_rows_) {
+          const int n = std::min(attn_rows_, T - r0);
+          rope_cache_attention(attn_ + size_t(r0) * cfg_.q_dim(), q_ + size_t(r0) * cfg_.q_dim(),
+                               k_ + size_t(r0) * cfg_.kv_dim(), v_ + size_t(r0) * cfg_.kv_dim(),
+                               kp, vp, rope_, lim_.max_seq_len, n, rpos + r0, rseq + r0, kv,
+                               s.chunks, s.chunk_tokens, workspace_, NH, NKV, HD, stream_);
+        }
       } else {
-        rope_and_cache(q_, k_, v_, kp, vp, rope_table_, max_seq_len_, T, row_pos_, row_seq_, kv,
-                       NH, NKV, HD, stream_);
-        if (s.prompt)
-          attention_prefill(attn_, q_, kp, vp, T, row_pos_, row_seq_, kv, NH, NKV, HD, stream_);
-        else
-          attention(attn_, q_, kp, vp, T, row_pos_, row_seq_, kv, s.chunks, s.chunk_tokens,
-                    workspace_, NH, NKV, HD, stream_);
+        rope_and_cache(q_, k_, v_, kp, vp, rope_, lim_.max_seq_len, T, rpos, rseq, kv, NH, NKV,
+                       HD, stream_);
+        if (s.prompt) {
+          attention_prefill(attn_, q_, kp, vp, T, rpos, rseq, kv, NH, NKV, HD, stream_);
+        } else {
+          for (int r0 = 0; r0 < T; r0 += attn_rows_) {
+            const int n = std::min(attn_rows_, T - r0);
+            attention(attn_ + size_t(r0) * cfg_.q_dim(), q_ + size_t(r0) * cfg_.q_dim(), kp, vp, n,
+                      rpos + r0, rseq + r0, kv, s.chunks, s.chunk_tokens, workspace_, NH, NKV, HD,
+                      stream_);
+          }
+        }
       }
       if (body_.after_attention) body_.after_attention(l, T, stream_);
+      if (after_layer) after_layer(l);
     }
+    if (body_.end) body_.end(T, s.logit_rows, stream_);
   }
 
-  /* Records one decode step of s.rows sequences (capture_graph,
-   * src/cuda/cuda_runner.cu:470-487). */
-  void capture_graph(const StepInfo& s) {
+  /* Records one decode step of s.rows sequences into a graph. */
+  hipGraphExec_t record(const StepInfo& s) {
     hipGraph_t graph = nullptr;
     check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
     try {
-      enqueue(s);
+      enqueue(s, nullptr);
     } catch (...) {
       (void)hipStreamEndCapture(stream_, &graph);
       if (graph) (void)hipGraphDestroy(graph);
@@ -383,7 +485,7 @@ class KvEngine {
     const hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     check(err, "hipGraphInstantiate");
-    graphs_[s.rows] = exec;
+    return exec;
   }
 
   void drop_graphs() {
@@ -391,38 +493,11 @@ class KvEngine {
     graphs_.clear();
   }
 
-  /* Row buffers for T rows and the split-K workspace for `chunks`, grown on
-   * demand; recorded graphs hold the old addresses, so growth drops them
-   * (reserve, src/cuda/cuda_runner.cu:492-541). */
-  void reserve(int T, int chunks) {
-    if (T > cap_rows_) {
-      drop_graphs();
-      for (void* p : {(void*)row_seq_, (void*)row_pos_, (void*)q_, (void*)k_, (void*)v_,
-                      (void*)attn_})
-        mem_.release(p);
-      cap_rows_ = std::max(T, 16);
-      const size_t n = size_t(cap_rows_);
-      row_seq_ = mem_.alloc<int>(n);
-      row_pos_ = mem_.alloc<int>(n);
-      q_ = mem_.alloc<float>(n * cfg_.q_dim());
-      k_ = mem_.alloc<float>(n * cfg_.kv_dim());
-      v_ = mem_.alloc<float>(n * cfg_.kv_dim());
-      attn_ = mem_.alloc<float>(n * cfg_.q_dim());
-      h_row_seq_.resize(n);
-      h_row_pos_.resize(n);
-    }
-    const size_t ws = chunks > 0
-        ? attention_workspace_bytes(T, cfg_.num_heads, cfg_.head_dim, chunks) : 0;
-    if (ws > cap_ws_) {
-      drop_graphs();
-      mem_.release(workspace_);
-      workspace_ = mem_.alloc<unsigned char>(ws);
-      cap_ws_ = ws;
-    }
-  }
-
   void release() {
     drop_graphs();
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (staged_) (void)hipEventDestroy(staged_);
+    staged_ = nullptr;
     if (stream_) (void)hipStreamDestroy(stream_);
     stream_ = nullptr;
     if (pages_) ie_pages_destroy(pages_);
@@ -430,28 +505,29 @@ class KvEngine {
   }
 
   KvConfig cfg_;
-  int max_batch_ = 1, max_seq_len_ = 0, num_pages_ = 0, max_pages_per_seq_ = 0;
-  bool use_graphs_ = true;
-  int kv_dtype_ = IE_KV_F32;
+  EngineLimits lim_;
+  int kv_dtype_;
+  bool use_graphs_;
   LayerBody body_;
   std::string name_;
-  DeviceMemory mem_;
-  hipStream_t stream_ = nullptr;
-  std::map<int, hipGraphExec_t> graphs_;  // decode graphs by batch size
-  StepInfo last_;
+  int chunk_tokens_ = 0, max_chunks_ = 0, attn_rows_ = 0, max_pages_per_seq_ = 0;
 
   ie_page_pool* pages_ = nullptr;  // free list, sequences, host page table
-  int32_t* tables_ = nullptr;      // device copy of the page table
-  float* rope_table_ = nullptr;    // [max_seq_len, head_dim] cos | sin
-  unsigned char *k_pool_ = nullptr, *v_pool_ = nullptr;  // [layer][page][row][kv_dim]
-  size_t layer_bytes_ = 0;
+  DeviceArena arena_;
+  PinnedBlock staging_;
+  hipStream_t stream_ = nullptr;
+  hipEvent_t staged_ = nullptr;    // the last input copy
+  std::map<std::pair<int, int>, hipGraphExec_t> graphs_;  // decode graphs by (rows, logit rows)
+  StepInfo last_;
+  int cur_rows_ = 0, cur_logit_rows_ = 0;
 
-  int cap_rows_ = 0;
-  size_t cap_ws_ = 0;
-  int *row_seq_ = nullptr, *row_pos_ = nullptr;
+  size_t layer_bytes_ = 0;
+  unsigned char* pools_ = nullptr;  // [layer][K | V][page][row][kv_dim]
+  int32_t* tables_ = nullptr;       // device copy of the page table
+  float* rope_ = nullptr;           // [max_seq_len, head_dim] cos | sin
+  int32_t* inputs_ = nullptr;       // the step's packed inputs
   float *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *attn_ = nullptr;
-  unsigned char* workspace_ = nullptr;  // flash-decoding partials (part_o + part_ml)
-  PinnedBuffer<int> h_row_seq_, h_row_pos_;
+  unsigned char* workspace_ = nullptr;  // flash-decoding partials
 };
 
 }  // namespace ie::hip

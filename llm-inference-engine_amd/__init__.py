@@ -71,6 +71,7 @@ _SIGS = {
     "ie_hip_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _i, _vp]),
     "ie_hip_gather_rows": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "ie_hip_gather_kv": (_i, [_vp, _vp, KvLayout, _i, _i, _i, _vp]),
+    "ie_hip_argmax_rows": (_i, [_vp, _vp, _i, _i, _vp]),
     "ie_hip_embedding": (_i, [_vp, _vp, Matrix, _i, _vp]),
     "ie_hip_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     "ie_hip_matmul": (_i, [_vp, _vp, Matrix, _vp, _i, _i, _vp]),
@@ -242,6 +243,12 @@ def attention_prefill(out, q, k_pool, v_pool, row_pos, row_seq, tables, max_page
 def gather_rows(dst, src, rows, stream=None) -> None:
     """dst[r] = src[rows[r]] (src/cuda/kernels.cuh:101-102)."""
     _check(lib().ie_hip_gather_rows(_ptr(dst), _ptr(src), _ptr(rows), rows.numel(), src.shape[-1],
+                                    _stream(stream)))
+
+
+def argmax_rows(out, logits, stream=None) -> None:
+    """out[r] = first index of the maximum of logits[r] (src/cuda/kernels.cuh:106)."""
+    _check(lib().ie_hip_argmax_rows(_ptr(out), _ptr(logits), logits.shape[0], logits.shape[1],
                                     _stream(stream)))
 
 

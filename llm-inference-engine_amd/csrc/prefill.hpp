@@ -13,7 +13,6 @@ int prefill_valu_launch(float* out, const float* q, const void* k_pool, const vo
 
 // QK^T and PV on MFMA (prefill_mfma.hip): 16-bit caches in their own type with
 // hi + lo operands, float32 caches on the f32 matrix instructions.
-bool prefill_mfma_enabled();
 bool prefill_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim);
 int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                         const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,

@@ -799,8 +799,6 @@ int launch_prefill_f32(const dim3 grid, float* out, const float* q, const float*
 
 }  // namespace
 
-bool prefill_mfma_enabled() { return true; }
-
 bool prefill_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim) {
   return (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16 || kv_dtype == IE_KV_F32) &&
          head_dim == 64 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 &&

@@ -249,7 +249,12 @@ int main(int argc, char** argv) {
     cfg.num_kv_heads = NKV;
     cfg.head_dim = HD;
     cfg.rope_theta = kTheta;
-    KvEngine eng(cfg, kMaxBatch, kMaxSeq, kPages, /*use_graphs=*/true, kv, h.body());
+    ie::hip::EngineLimits lim;
+    lim.max_batch = kMaxBatch;
+    lim.max_seq_len = kMaxSeq;
+    lim.num_pages = kPages;
+    lim.step_rows = kCap;
+    KvEngine eng(cfg, lim, kv, /*use_graphs=*/true, h.body());
     h.eng = &eng;
     h.fill_pools();
     std::printf("device: %s\n", eng.device_name().c_str());

@@ -32,6 +32,21 @@ using namespace ie::hip;
 
 namespace {
 
+/* One layer's weights on the host, BF16 bits in the reference's layout. */
+struct HostLayer {
+  std::vector<float> input_norm, post_norm;    // [hidden]
+  std::vector<uint16_t> wq, wk, wv, wo;        // [q_dim, hidden], [kv_dim, hidden] x2, [hidden, q_dim]
+  std::vector<float> bq, bk, bv;               // [q_dim], [kv_dim] x2
+  std::vector<uint16_t> w_gate, w_up, w_down;  // [inter, hidden] x2, [hidden, inter]
+};
+
+/* The model's weights on the host; the LM head is the embedding (tied). */
+struct HostModel {
+  std::vector<uint16_t> embed;    // [vocab, hidden]
+  std::vector<float> final_norm;  // [hidden]
+  std::vector<HostLayer> layers;
+};
+
 constexpr int kLayers = 2, NH = 14, NKV = 2, HD = 64, QD = NH * HD, KVD = NKV * HD;
 constexpr int H = 896, I = 4864, V = 512, kMaxBatch = 4, kMaxSeq = 256, kPages = 64;
 constexpr float kTheta = 1e6f, kEps = 1e-6f;
@@ -155,6 +170,56 @@ HostModel random_model(std::mt19937& rng) {
   return m;
 }
 
+/* The device-side view of a HostModel: BF16 as stored, or every matrix
+ * quantized to INT8 with row scales exactly as the CPU side quantizes it. */
+struct Upload {
+  std::vector<std::vector<int8_t>> q;
+  std::vector<std::vector<float>> s;
+  ModelView view;
+
+  MatrixView matrix(const std::vector<uint16_t>& w, int rows, int cols, bool int8) {
+    MatrixView m;
+    m.rows = rows;
+    m.cols = cols;
+    if (!int8) {
+      m.data = w.data();
+      return m;
+    }
+    std::vector<float> f(w.size());
+    for (size_t i = 0; i < w.size(); ++i) f[i] = orc_bf16_to_f32(w[i]);
+    q.emplace_back(w.size());
+    s.emplace_back(rows);
+    orc_quantize_i8(q.back().data(), s.back().data(), f.data(), rows, cols);
+    m.data = q.back().data();
+    m.scale = s.back().data();
+    m.int8 = true;
+    return m;
+  }
+
+  Upload(const HostModel& h, bool int8) {
+    q.reserve(64);
+    s.reserve(64);
+    view.embed = matrix(h.embed, V, H, int8);
+    view.final_norm = h.final_norm.data();
+    for (const HostLayer& L : h.layers) {
+      LayerView l;
+      l.input_norm = L.input_norm.data();
+      l.post_norm = L.post_norm.data();
+      l.wq = matrix(L.wq, QD, H, int8);
+      l.wk = matrix(L.wk, KVD, H, int8);
+      l.wv = matrix(L.wv, KVD, H, int8);
+      l.wo = matrix(L.wo, H, QD, int8);
+      l.bq = L.bq.data();
+      l.bk = L.bk.data();
+      l.bv = L.bv.data();
+      l.w_gate = matrix(L.w_gate, I, H, int8);
+      l.w_up = matrix(L.w_up, I, H, int8);
+      l.w_down = matrix(L.w_down, H, I, int8);
+      view.layers.push_back(l);
+    }
+  }
+};
+
 template <class T>
 std::vector<T> download(const void* d, size_t n) {
   std::vector<T> h(n);
@@ -176,28 +241,35 @@ int main(int argc, char** argv) {
   ModelShape shape;
   shape.vocab = V;
   try {
-    DecoderModel model(cfg, shape, host, /*max_rows=*/64, int8);
-    KvEngine eng(cfg, kMaxBatch, kMaxSeq, kPages, /*use_graphs=*/true, kv);
+    EngineLimits lim;
+    lim.max_batch = kMaxBatch;
+    lim.max_seq_len = kMaxSeq;
+    lim.num_pages = kPages;
+    lim.step_rows = 64;
+    lim.logit_rows = 64;
+    KvEngine eng(cfg, lim, kv, /*use_graphs=*/true);
+    const Upload up(host, int8);
+    DecoderModel model(cfg, shape, up.view, eng.limits().step_rows, eng.limits().logit_rows);
     eng.set_body(model.body(eng));
     Cpu cpu(host, kv, eng.layer_pool_bytes(), int8);
-    float* d_logits = nullptr;
-    check(hipMalloc(&d_logits, size_t(64) * V * sizeof(float)), "hipMalloc");
     std::uniform_int_distribution<int> tok(0, V - 1);
 
+    // One step through the engine, then the same step on the CPU; every row's
+    // residual stream and logits compared.
     auto run_step = [&](const std::string& what, const std::vector<int32_t>& seqs,
                         const std::vector<int32_t>& pos, bool prefill) {
       const int T = int(seqs.size());
       std::vector<int32_t> ids(T);
       for (auto& id : ids) id = tok(rng);
-      model.embed(ids, eng.stream());
-      if (prefill) eng.prefill(seqs[0], T);
-      else eng.decode(std::vector<int>(seqs.begin(), seqs.end()));
-      model.logits(d_logits, T, T, eng.stream());
-      check(hipStreamSynchronize(eng.stream()), "sync");
+      std::vector<int> all(T);
+      for (int i = 0; i < T; ++i) all[i] = i;
+      eng.run(std::vector<int>(seqs.begin(), seqs.end()), std::vector<int>(pos.begin(), pos.end()),
+              ids, all, /*decode=*/!prefill);
+      eng.sync();
       std::vector<float> x_ref, lg_ref;
       cpu.step(ids, pos, seqs, eng.host_tables(), eng.max_pages_per_seq(), x_ref, lg_ref);
       const std::vector<float> x = download<float>(model.x(), size_t(T) * H);
-      const std::vector<float> lg = download<float>(d_logits, size_t(T) * V);
+      const std::vector<float> lg = download<float>(model.logits(), size_t(T) * V);
       double mae = 0;
       size_t worst = 0;
       const double rx = orc_compare(x.data(), x_ref.data(), x.size(), &mae, &worst);
@@ -206,6 +278,7 @@ int main(int argc, char** argv) {
       std::snprintf(buf, sizeof(buf), "%s: residual rel %.2e, logits rel %.2e (graph %d)",
                     what.c_str(), rx, rl, int(eng.last_step().graph));
       result(rx <= tol && rl <= tol && std::isfinite(rx) && std::isfinite(rl), buf);
+      return lg;
     };
 
     const int s0 = eng.open_sequence(), s1 = eng.open_sequence();
@@ -217,7 +290,18 @@ int main(int argc, char** argv) {
     for (int i = 0; i < 3; ++i)
       run_step("decode batch 2, step " + std::to_string(i), {s0, s1}, {40 + i, 17 + i}, false);
     run_step("decode batch 1", {s1}, {20}, false);
-    check(hipFree(d_logits), "hipFree");
+
+    // The device argmax of the last step's logits: the CPU scan's choice.
+    {
+      const std::vector<float> lg = download<float>(model.logits(), V);
+      model.argmax(1, eng.stream());
+      eng.sync();
+      const int32_t got = download<int32_t>(model.tokens(), 1)[0];
+      int32_t want = 0;
+      for (int i = 1; i < V; ++i)
+        if (lg[i] > lg[want]) want = i;
+      result(got == want, "argmax of the logits (device) == first strict maximum (host scan)");
+    }
   } catch (const std::exception& e) {
     result(false, std::string("exception: ") + e.what());
   }
