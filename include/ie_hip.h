@@ -135,6 +135,22 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
                      int num_chunks, int chunk_tokens, void* workspace, int n_heads,
                      int n_kv_heads, int head_dim, hipStream_t stream);
 
+/* ie_hip_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * split-K partials go to a fixed device array of IE_HIP_NOALLOC_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends; a
+ * call needing more (ie_hip_attention_workspace_bytes(T, n_heads, head_dim,
+ * num_chunks) above the limit: 64 rows x 14 heads hold up to 70 chunks) fails with
+ * EINVAL and the message says so. It allocates and frees nothing. Calls that
+ * overlap on one GPU share the array and race: serialise them (one stream).
+ * Results are bit-identical to ie_hip_attention's. */
+#define IE_HIP_NOALLOC_SCRATCH_BYTES (16u << 20)
+int ie_hip_attention_noalloc(float* out, const float* q, const void* k_pool, const void* v_pool,
+                             int T, const int32_t* row_pos, const int32_t* row_seq,
+                             ie_kv_layout kv, int num_chunks, int chunk_tokens, int n_heads,
+                             int n_kv_heads, int head_dim, hipStream_t stream);
+
 /* ------------------------------------------ decode step in one launch ---
  * ie_hip_rope_and_cache followed by ie_hip_attention, in one launch: the
  * reference's per-layer decode sequence rope_and_cache + attention

@@ -64,6 +64,8 @@ _SIGS = {
     "ie_hip_attention_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i]),
     "ie_hip_attention": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _vp, _i, _i, _i,
                               _vp]),
+    "ie_hip_attention_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _i, _i,
+                                      _i, _vp]),
     "ie_hip_rope_cache_attention_supported": (_i, [_i, _i, _i, _i, _i]),
     "ie_hip_rope_cache_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp,
                                          KvLayout, _i, _i, _vp, _i, _i, _i, _vp]),
@@ -203,6 +205,22 @@ def attention(out, q, k_pool, v_pool, row_pos, row_seq, tables, max_pages: int, 
     _check(lib().ie_hip_attention(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), T, _ptr(row_pos),
                                   _ptr(row_seq), kv, num_chunks, chunk_tokens, _ptr(workspace),
                                   n_heads, n_kv_heads, head_dim, _stream(stream)))
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # IE_HIP_NOALLOC_SCRATCH_BYTES
+
+
+def attention_noalloc(out, q, k_pool, v_pool, row_pos, row_seq, tables, max_pages: int,
+                      num_chunks: int, chunk_tokens: int, n_heads: int, n_kv_heads: int,
+                      head_dim: int, stream=None) -> None:
+    """attention() with the library's fixed device scratch in place of a workspace."""
+    T = row_pos.numel()
+    kv = layout(tables, max_pages, k_pool.numel() // (PAGE_SIZE * n_kv_heads * head_dim),
+                _dtype_code(k_pool))
+    _check(lib().ie_hip_attention_noalloc(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), T,
+                                          _ptr(row_pos), _ptr(row_seq), kv, num_chunks,
+                                          chunk_tokens, n_heads, n_kv_heads, head_dim,
+                                          _stream(stream)))
 
 
 def rope_cache_attention_supported(kv_dtype: int, n_heads: int, n_kv_heads: int, head_dim: int,

@@ -21,6 +21,7 @@
 //   chunk writes (o, m, l) and decode_merge_kernel combines them:
 //   M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L.
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
 #include "decode.hpp"
@@ -536,6 +537,70 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
   return decode_valu(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
                      workspace, n_heads, n_kv_heads, stream);
 }
+
+}  // extern "C"
+
+// ------------------------------------------------- no-allocation variant ---
+// ie_hip_attention for callers that cannot allocate (HIP graph capture, tight
+// serving loops): the split-K partials go to `scratch`, a fixed device array of
+// IE_HIP_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until
+// the process ends. Host code never passes `scratch` itself (its name is a host
+// stand-in, not a device address): the first call on a device looks up that
+// device's copy with hipGetSymbolAddress, once, and every later call passes
+// the address kept for it. The partials need no initialisation (a call reads
+// only the slots it wrote), so nothing is cleared. Calls that overlap on one
+// GPU share the array and race.
+static __device__ __align__(256) unsigned char scratch[IE_HIP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "attention_noalloc: hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(IE_HIP_EINVAL, "attention_noalloc: device index above 63");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                           "attention_noalloc: hipGetSymbolAddress(scratch)"))
+      return rc;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return IE_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int ie_hip_attention_noalloc(float* out, const float* q, const void* k_pool,
+                                        const void* v_pool, int T, const int32_t* row_pos,
+                                        const int32_t* row_seq, ie_kv_layout kv, int num_chunks,
+                                        int chunk_tokens, int n_heads, int n_kv_heads,
+                                        int head_dim, hipStream_t stream) {
+  clear_error();
+  if (T < 0 || num_chunks <= 0 || n_heads <= 0 || head_dim <= 0)
+    return fail(IE_HIP_EINVAL, "attention_noalloc: bad row, chunk or head count");
+  if (T == 0) return IE_HIP_OK;
+  const size_t need = workspace_bytes(T, n_heads, head_dim, num_chunks);
+  if (need > IE_HIP_NOALLOC_SCRATCH_BYTES)
+    return fail(IE_HIP_EINVAL,
+                "attention_noalloc: " + std::to_string(T) + " rows x " + std::to_string(n_heads) +
+                    " heads x " + std::to_string(num_chunks) + " chunks need " +
+                    std::to_string(need) + " bytes of split-K scratch; the fixed scratch holds " +
+                    std::to_string(size_t(IE_HIP_NOALLOC_SCRATCH_BYTES)) +
+                    " (use ie_hip_attention with a workspace)");
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  return ie_hip_attention(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks,
+                          chunk_tokens, ws, n_heads, n_kv_heads, head_dim, stream);
+}
+
+extern "C" {
 
 static bool fused_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim,
                             int chunk_tokens) {
