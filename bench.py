@@ -4,25 +4,33 @@
 Default workload (the headline metric): flash-decoding paged
 attention, batch 64, ragged contexts L ~ U[128, 4096], GQA 14 query / 2 KV
 heads, head_dim 64, f16 KV in 16-token pages, block tables a seeded permutation
-of a 65,536-page pool, 512-token split-K partitions with a log-sum-exp merge.
+of a 65,536-page pool, split-K partitions merged by log-sum-exp.
 
-One step = one attention launch over the whole batch, inputs resident in HBM.
+One step = one attention call over the whole batch, inputs resident in HBM.
 Each step reads a different layer's pools (--layers, default 8 x 537 MB), so
 the >= 2 x 256 MB working set defeats the 256 MB Infinity Cache and the rate
 is HBM, not MALL. value = algorithmic bytes / time (GB/s):
     per row  512*L (K+V, f16) + 3584 (q) + 3584 (out) + 4*ceil(L/16) (page ids) + 8
-The roofline fraction is against the nominal 8 TB/s. Its duration (us_per_launch) is
-the graph-timed time per entry-point call: every kernel the call launches (named in
-roofline.kernel; for attention the partial kernel and the split-K merge) and the launch
-gaps between calls. The rocprofv3 kernel trace under profiles/ gives each kernel's own
-average; they add up to this figure less the gaps. Bracketing one kernel with HIP events
-was tried and dropped: event records around a launch slowed the kernel itself (the
-prefill 71 -> 86 us). cpu_baseline times the
-reference's own CPU attention (oracle/_ref: src/ops.cpp + src/threadpool.cpp,
--O3 -mavx2 -mfma) on the same batch, rows gathered to contiguous fp32 first
-(gather timed separately), on this host's cores.
+Timing: the `steps` calls are recorded into one HIP graph, replayed at least 5 times
+(and at least 100 calls in all), each replay between HIP events; the median replay
+gives ms_per_step ("timing" in the line). The roofline fraction is against the
+nominal 8 TB/s; its duration (us_per_launch) is the time per entry-point call, every
+kernel the call launches (roofline.kernel) and the gaps between calls. The rocprofv3
+kernel trace under profiles/ gives each kernel's own average.
+
+The default line also carries:
+  probe / ceiling_gbs  hand-written read kernels (llm-inference-engine_amd/probe): a 70 MB
+                       and a 256 MB contiguous stream over rotated buffers, and the page
+                       walk of this very batch with no arithmetic;
+  config2_append       the RoPE + paged append at 64 and 131,072 rows per launch;
+  config5_prefill      the 4,000-token prefill's MFMA fraction;
+  cpu_baseline         the reference's own CPU attention (oracle/_ref: src/ops.cpp +
+                       src/threadpool.cpp, -O3 -mavx2 -mfma) on the same batch, rows
+                       gathered to contiguous fp32 first (timed apart), with the host's
+                       physical core count and the threads used.
 
 Other configs print the same JSON shape for the tables in DESIGN.md:
+  --config 1  the reference's own CPU case (one layer, 512 positions, fp32), GPU and CPU
   --config 2  RoPE + paged append, 64 rows (+ --sweep: rows per launch up to 131,072)
   --config 4  long-context decode, 24 layers, batch 1, 32k context, bf16
   --config 5  mixed step: 48 decode rows + a 4,000-token prefill (MFMA), f16
@@ -80,6 +88,9 @@ def fill_pool(torch, n_rows, kv, gen, dev):
 EAGER = False  # --eager: launch every timed step from Python (for counter collection)
 
 
+TIMING = {}  # how the last time_steps call was measured (reported in the JSON line)
+
+
 def time_steps(torch, step, steps, warmup, stream):
     """Runs `warmup` eager steps, then times exactly `steps` steps, in ms per step.
 
@@ -87,33 +98,48 @@ def time_steps(torch, step, steps, warmup, stream):
     ctypes launch costs about as much host time as the kernels take on the GPU, so
     eager launches would measure the host. The library allocates and memsets nothing
     inside a call, so its launches record as plain kernel nodes. The graph is replayed
-    once untimed, then once between two events on the launch stream.
+    once untimed, then at least 5 times (and at least 100 steps in all), each replay
+    between two HIP events on the launch stream with a synchronize on both sides; the
+    result is the median replay's time per step.
     """
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    if EAGER:
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(steps):
-            step(warmup + i)
-        end.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            step(warmup + i)
-    graph.replay()
-    torch.cuda.synchronize()
+    replays = max(5, -(-100 // max(steps, 1)))
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    graph.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per step
+    per_step = []
+    if EAGER:
+        for r in range(replays):
+            torch.cuda.synchronize()
+            start.record(stream)
+            for i in range(steps):
+                step(warmup + r * steps + i)
+            end.record(stream)
+            torch.cuda.synchronize()
+            per_step.append(start.elapsed_time(end) / steps)
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(steps):
+                step(warmup + i)
+        graph.replay()
+        torch.cuda.synchronize()
+        for _ in range(replays):
+            torch.cuda.synchronize()
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
+            torch.cuda.synchronize()
+            per_step.append(start.elapsed_time(end) / steps)
+    med = float(np.median(per_step))
+    TIMING.clear()
+    TIMING.update({"replays": replays, "steps_per_replay": steps, "launches": replays * steps,
+                   "median_ms_per_step": round(med, 6),
+                   "mean_ms_per_step": round(float(np.mean(per_step)), 6),
+                   "min_ms_per_step": round(float(np.min(per_step)), 6),
+                   "max_ms_per_step": round(float(np.max(per_step)), 6)})
+    return med
 
 
 def cpu_baseline_decode(O, lens, k_host, v_host, tables, kv, q_host, budget_s=10.0):
@@ -151,6 +177,8 @@ def cpu_baseline_decode(O, lens, k_host, v_host, tables, kv, q_host, budget_s=10
         "value": round(decode_bytes(lens, KV_BYTES[kv]) / t / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
+        "threads": cores,
+        "physical_cores": O.physical_cores(),
         "kind": "reference" if use_ref else "port",
         "sample": (f"the full batch ({len(lens)} rows, same contexts), {batches} passes in "
                    f"{time.perf_counter() - t_start:.1f} s; median attention time per batch "
@@ -202,7 +230,8 @@ def cpu_baseline_append(O, q, k, v, pos, kv, budget_s=3.0):
             break
     t = float(np.median(times))
     per_row = 1024 + 2 * KVD * KV_BYTES[kv] + 8 + 4 + 2 * QD * 4
-    return {"value": round(T * per_row / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": round(T * per_row / t / 1e9, 3), "unit": "GB/s", "cores": 1, "threads": 1,
+            "physical_cores": O.physical_cores(), "kind": "port",
             "sample": f"the 64 rows with q, {len(times)} batches; median {t * 1e6:.1f} us per batch "
                       f"(oracle/oracle.cpp, single thread, as the reference's rope runs)",
             "us_per_launch": round(t * 1e6, 2)}
@@ -231,6 +260,7 @@ def cpu_baseline_long(O, k_pools, v_pools, tabs, q, L, kv, layers, budget_s=8.0)
     t = float(np.median(attn)) * layers
     per_layer = 2 * KVD * KV_BYTES[kv] * L + 2 * QD * 4 + 4 * (L // PAGE) + 8
     return {"value": round(layers * per_layer / t / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "threads": cores, "physical_cores": O.physical_cores(),
             "kind": "reference" if O.ref_available() else "port",
             "sample": f"{n} layers' attention over 32,768 positions (gather to contiguous fp32 "
                       f"excluded, median {float(np.median(gath)) * 1e3:.1f} ms); step = median "
@@ -289,7 +319,8 @@ def cpu_baseline_model(O, layer_bits, norms, embed_bits, x, kc, vc, pos, layers,
         R.ref_matrix_destroy(ctypes.c_void_p(m))
     t_layer = float(np.median(dense)) + float(np.mean(attn)) * B
     t = layers * t_layer + t_lm
-    return {"value": round(B / t, 2), "unit": "tok/s", "cores": cores,
+    return {"value": round(B / t, 2), "unit": "tok/s", "cores": cores, "threads": cores,
+            "physical_cores": O.physical_cores(),
             "kind": "reference" if O.ref_available() else "port",
             "sample": f"one layer's dense ops for {B} rows (median of {reps}: "
                       f"{float(np.median(dense)) * 1e3:.1f} ms), attention of {len(kc)} rows "
@@ -321,6 +352,7 @@ def cpu_baseline_mixed(O, pq_h, kc_pf, vc_pf, P, dq_h, dec_kv, budget_s=10.0):
     t_pf = float(np.median(pf)) * flops_all / flops_sub
     t = t_pf + float(np.median(dc))
     return {"value": round((len(dec_kv) + P) / t, 1), "unit": "rows/s", "cores": cores,
+            "threads": cores, "physical_cores": O.physical_cores(),
             "kind": "reference" if O.ref_available() else "port",
             "sample": f"prompt rows {P - sub}..{P - 1} ({len(pf)} passes, scaled to the 4,000-row "
                       f"prefill by causal flops) + the 48 decode rows; gathers excluded",
@@ -357,6 +389,7 @@ def bench_decode(args, torch, ie, O):
                      NH, NKV, HD)
 
     ms = time_steps(torch, step, args.steps, args.warmup, stream)
+    timing = dict(TIMING)
     nbytes = decode_bytes(lens, KV_BYTES[kv])
     gbs = nbytes / (ms * 1e-3) / 1e9
 
@@ -388,11 +421,18 @@ def bench_decode(args, torch, ie, O):
                                + " + decode_merge_kernel (one ie_hip_attention call)",
                      "us_per_launch": round(ms * 1e3, 3)},
         "algorithmic_bytes_per_step": nbytes,
+        "timing": timing,
         "warm_mall": {"ms_per_step": round(ms_warm, 5),
                       "gbs": round(nbytes / (ms_warm * 1e-3) / 1e9, 2),
                       "note": "one layer's pools repeated: pages resident in the Infinity Cache; "
                               "not the metric"},
     }
+    if not args.no_probe:
+        probe = hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct, kv)
+        if probe:
+            res["probe"] = probe
+            res["ceiling_gbs"] = probe["ceiling_gbs"]
+            res["frac_of_ceiling"] = round(gbs / probe["ceiling_gbs"], 4)
     if not args.no_cpu:
         kh = O.widen_kv(k_pools[0].cpu().view(torch.int16).numpy().view(np.uint16), KV_CODES[kv]) \
             if kv != "f32" else k_pools[0].cpu().numpy()
@@ -416,7 +456,9 @@ def bench_append(args, torch, ie, O):
     table = ie.rope_table(max_pos, HD, THETA).to(dev)
     stream = torch.cuda.current_stream()
     sweep = []
-    for rows in ([64] + ([256, 1024, 4096, 16384, 65536, 131072] if args.sweep else [])):
+    rows_list = getattr(args, "append_rows", None) or \
+        ([64] + ([256, 1024, 4096, 16384, 65536, 131072] if args.sweep else []))
+    for rows in rows_list:
         seqs = max(1, rows // 64)
         max_pages = num_pages // seqs
         tables = rng.permutation(num_pages)[:seqs * max_pages].astype(np.int32).reshape(seqs, -1)
@@ -649,6 +691,196 @@ def bench_mixed(args, torch, ie, O):
     return res
 
 
+def _probe_lib():
+    """libie_probe.so: the hand-written HBM probes (llm-inference-engine_amd/probe)."""
+    path = os.path.join(ROOT, "llm-inference-engine_amd", "libie_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    lib.ie_probe_read.argtypes = [vp, ctypes.c_size_t, i, vp, vp]
+    lib.ie_probe_pages.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, vp, vp]
+    return lib
+
+
+def hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct, kv):
+    """The read rate this device reaches with no arithmetic, measured as the decode call
+    is (graph replays, median), with the kernels of llm-inference-engine_amd/probe:
+      read_70MB   contiguous 16-byte loads of 70 MB (one attention call's size), over 8
+                  buffers in turn (560 MB, twice the 256 MB Infinity Cache);
+      read_256MB  the same for 256 MB over 4 buffers (1 GB): the large-stream rate;
+      page_walk   config 3's own grid and block tables over the same rotated pools,
+                  reading every K and V page of every (row, chunk) and nothing else.
+    ceiling_gbs is read_70MB: what one 70 MB read of this device achieves per launch."""
+    lib = _probe_lib()
+    if lib is None:
+        return None
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
+    sp = lambda: torch.cuda.current_stream().cuda_stream  # the capture stream while recording
+    out = {}
+    for mb, nbuf in ((70, 8), (256, 4)):
+        nbytes = mb * 1000 * 1000 // 16 * 16
+        bufs = [torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=dev)
+                for _ in range(nbuf)]
+
+        best = None
+        for per_cu in (4, 8, 16, 32):  # workgroups of 256 threads per compute unit
+            def step(i, bufs=bufs, nbytes=nbytes, nbuf=nbuf, wgs=per_cu * cus):
+                rc = lib.ie_probe_read(bufs[i % nbuf].data_ptr(), nbytes, wgs, sink.data_ptr(),
+                                       sp())
+                assert rc == 0
+
+            ms = time_steps(torch, step, max(args.steps, 40), 5, stream)
+            if best is None or ms < best[0]:
+                best = (ms, per_cu)
+        ms = best[0]
+        out[f"read_{mb}MB_gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        out[f"read_{mb}MB_us"] = round(ms * 1e3, 3)
+        out[f"read_{mb}MB_workgroups_per_cu"] = best[1]
+        del bufs
+    rows, chunks = [], []
+    for r, L in enumerate(lens):
+        for c in range((int(L) + ct - 1) // ct):
+            rows.append(r)
+            chunks.append(c)
+    d_r = torch.tensor(rows, dtype=torch.int32, device=dev)
+    d_c = torch.tensor(chunks, dtype=torch.int32, device=dev)
+    d_len = torch.tensor([int(L) for L in lens], dtype=torch.int32, device=dev)
+    page_bytes = PAGE * KVD * KV_BYTES[kv]
+    walk_bytes = 2 * page_bytes * sum((int(L) + PAGE - 1) // PAGE for L in lens)
+
+    def walk(i):
+        l = i % len(k_pools)
+        rc = lib.ie_probe_pages(k_pools[l].data_ptr(), v_pools[l].data_ptr(), d_tab.data_ptr(),
+                                d_r.data_ptr(), d_c.data_ptr(), d_len.data_ptr(), len(rows),
+                                max_pages, ct, page_bytes, sink.data_ptr(), sp())
+        assert rc == 0
+
+    ms = time_steps(torch, walk, max(args.steps, 40), 5, stream)
+    out["page_walk_gbs"] = round(walk_bytes / (ms * 1e-3) / 1e9, 1)
+    out["page_walk_us"] = round(ms * 1e3, 3)
+    out["page_walk_bytes"] = walk_bytes
+    out["ceiling_gbs"] = out["read_70MB_gbs"]
+    return out
+
+
+def extra_targets(args, torch, ie, O):
+    """The north star's other two targets, measured in the default run so that one line
+    carries all three: the RoPE + append (config 2: 64 rows, and 131,072 rows per launch,
+    K/V only) and the 4,000-token prefill's MFMA fraction (config 5)."""
+    import copy
+    sub = copy.copy(args)
+    sub.no_cpu, sub.kv, sub.chunk_tokens, sub.sweep = True, None, None, False
+    sub.steps, sub.warmup = max(20, min(args.steps, 100)), 5
+    sub.append_rows = [64, 131072]
+    app = bench_append(sub, torch, ie, O)
+    pts = {s["rows"]: s for s in app["sweep"] if not s["with_q"]}
+    mix = bench_mixed(sub, torch, ie, O)
+    return {
+        "config2_append": {
+            "rows_64": {"us_per_launch": pts[64]["us_per_launch"], "gbs": pts[64]["gbs"],
+                        "frac": round(pts[64]["gbs"] / HBM_PEAK_GBS, 4)},
+            "rows_131072": {"us_per_launch": pts[131072]["us_per_launch"],
+                            "gbs": pts[131072]["gbs"],
+                            "frac": round(pts[131072]["gbs"] / HBM_PEAK_GBS, 4)},
+            "target_frac": 0.60, "bytes_per_row": 1548,
+            "kernel": "rope_append_kernel (ie_hip_rope_and_cache, K/V only)"},
+        "config5_prefill": {
+            "us_per_launch": mix["roofline"]["us_per_launch"],
+            "tflops": mix["roofline"]["achieved"], "frac": mix["roofline"]["frac"],
+            "mixed_step_ms": mix["ms_per_step"], "decode_part_gbs": mix["decode_part_gbs"],
+            "kernel": mix["roofline"]["kernel"]},
+    }
+
+
+def bench_config1(args, torch, ie, O):
+    """Config 1, the reference's own CPU case: one layer of one sequence, Qwen2.5-0.5B's
+    attention shape -- rope(q) and rope(k) at position 511, k/v appended to a contiguous
+    fp32 cache whose rows 0..510 are N(0,1), then decode attention over the 512 positions
+    (src/model.cpp:62-77, src/ops.cpp:34-108). The CPU side runs the reference's own
+    rope and attention (oracle/_ref) on its thread pool; the GPU side runs the same work on
+    the paged path (f32 KV, 32 pages): ie_hip_rope_and_cache + ie_hip_attention."""
+    rng = np.random.default_rng(args.seed)
+    L, pos = 512, 511
+    q = rng.standard_normal((1, QD), dtype=np.float32)
+    k = rng.standard_normal((1, KVD), dtype=np.float32)
+    v = rng.standard_normal((1, KVD), dtype=np.float32)
+    kc = rng.standard_normal((L, KVD), dtype=np.float32)
+    vc = rng.standard_normal((L, KVD), dtype=np.float32)
+    dev = torch.device("cuda:0")
+    # GPU: the same step on pages.
+    pages = L // PAGE
+    tables = rng.permutation(pages).astype(np.int32)[None, :]
+    kp = np.zeros((pages * PAGE, KVD), np.float32)
+    vp = np.zeros((pages * PAGE, KVD), np.float32)
+    for i in range(pages):
+        kp[tables[0, i] * PAGE:(tables[0, i] + 1) * PAGE] = kc[i * PAGE:(i + 1) * PAGE]
+        vp[tables[0, i] * PAGE:(tables[0, i] + 1) * PAGE] = vc[i * PAGE:(i + 1) * PAGE]
+    k_pool, v_pool = torch.from_numpy(kp).to(dev), torch.from_numpy(vp).to(dev)
+    d_tab = torch.from_numpy(tables).to(dev)
+    d_pos = torch.tensor([pos], dtype=torch.int32, device=dev)
+    d_seq = torch.zeros(1, dtype=torch.int32, device=dev)
+    dq0 = torch.from_numpy(q).to(dev)
+    dq = dq0.clone()
+    dk, dv = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+    table = ie.rope_table(L, HD, THETA).to(dev)
+    ct = ie.attention_chunk_tokens(1, L, ie.KV_F32)
+    nc = ie.attention_chunks(L, ct)
+    ws = ie.attention_workspace(1, NH, HD, nc)
+    out = torch.empty((1, QD), device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        dq.copy_(dq0)
+        ie.rope_and_cache(dq, dk, dv, k_pool, v_pool, table, d_pos, d_seq, d_tab, pages, NH, NKV,
+                          HD)
+        ie.attention(out, dq, k_pool, v_pool, d_pos, d_seq, d_tab, pages, nc, ct, ws, NH, NKV, HD)
+
+    ms = time_steps(torch, step, args.steps, args.warmup, stream)
+    timing = dict(TIMING)
+    nbytes = 1024 * L + 2 * QD * 4 + 4 * pages + 8 + 1548 + 2 * QD * 4
+    res = {
+        "metric": "config 1: one decode step of one layer, 512 positions, fp32 KV (tok/s)",
+        "value": round(1 / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "config 1: rope(q), rope(k) at 511, append, attention over 512 "
+                               "positions, 14q/2kv heads of 64, f32 KV", "seed": args.seed,
+                   "chunk_tokens": ct},
+        "timing": timing,
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
+                     "traffic": None, "kernel": "rope_append_kernel + decode_partial_mfma_f32 "
+                                                "(+ merge): latency-bound at this size",
+                     "us_per_launch": round(ms * 1e3, 3)},
+    }
+    if not args.no_cpu and O.ref_available():
+        cores = O.physical_cores()
+        O.ref().ref_set_num_threads(cores)  # the reference's pool: one thread per core
+        times, t_start = [], time.perf_counter()
+        while True:
+            t0 = time.perf_counter()
+            qr = O.ref_rope(q, NH, HD, pos, THETA)
+            kr = O.ref_rope(k, NKV, HD, pos, THETA)
+            kc[pos] = kr[0]
+            vc[pos] = v[0]
+            O.ref_attention(qr, kc, vc, pos, NH, NKV, HD)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - t_start >= min(args.cpu_seconds, 5.0) and len(times) >= 50:
+                break
+        t = float(np.median(times))
+        res["cpu_baseline"] = {
+            "value": round(1 / t, 1), "unit": "tok/s", "cores": cores, "threads": cores,
+            "physical_cores": cores, "kind": "reference",
+            "sample": f"the whole case, {len(times)} runs, median {t * 1e6:.1f} us (the "
+                      f"reference's rope + attention on its thread pool; the append is a copy)"}
+    return res
+
+
 def traffic_from_profiles(key: str, kv: str, default_kv: str, args):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE runs, as committed
     under profiles/: `key` for the workload's default KV type, `key_<kv>` for another.
@@ -828,7 +1060,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5, 6])
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5, 6])
     ap.add_argument("--kv", choices=list(KV_CODES), default=None)
     ap.add_argument("--chunk-tokens", type=int, default=None)
     ap.add_argument("--layers", type=int, default=8)
@@ -842,6 +1074,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true", help="config 2: rows-per-launch sweep")
     ap.add_argument("--probe", action="store_true", help="also measure device copy bandwidth")
+    ap.add_argument("--no-probe", action="store_true",
+                    help="config 3: skip the HBM read probes (ceiling_gbs)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="config 3: skip the config-2 append and config-5 prefill keys")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed steps one by one instead of replaying a graph "
                          "(host-bound timing; for rocprofv3 counter runs)")
@@ -870,9 +1106,11 @@ def main():
         print(json.dumps({"measured_copy_gbs": copy_probe(torch), "copy_bytes": 2 << 30}),
               flush=True)
         return
-    res = {2: bench_append, 3: bench_decode, 4: bench_long, 5: bench_mixed,
+    res = {1: bench_config1, 2: bench_append, 3: bench_decode, 4: bench_long, 5: bench_mixed,
            6: bench_model}[args.config](
         args, torch, ie, O)
+    if args.config == 3 and not args.no_extras and args.impl == "auto" and not args.kv:
+        res.update(extra_targets(args, torch, ie, O))
     if args.probe:
         res["measured_copy_gbs"] = copy_probe(torch)
     print(json.dumps(res), flush=True)

@@ -70,7 +70,25 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_probe(verbose)
     return LIB
+
+
+PROBE_SRC = os.path.join(PKG, "probe", "hbm_probe.hip")
+PROBE_LIB = os.path.join(PKG, "libie_probe.so")
+
+
+def build_probe(verbose: bool = False) -> str:
+    """The HBM probes bench.py times next to the decode kernel (measurement only)."""
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [hipcc(), *CFLAGS, "-shared", PROBE_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"probe build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    if verbose:
+        print(f"built {PROBE_LIB}")
+    return PROBE_LIB
 
 
 if __name__ == "__main__":
