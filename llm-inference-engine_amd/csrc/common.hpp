@@ -28,7 +28,12 @@ int check_launch(const char* kernel);
 // binary16 subnormals kept in the default denormal mode).
 // bf16: round to nearest even by integer add, inf/NaN truncated, exactly the
 // host rule of the reference (src/matrix.cpp:46-52).
+// f is made opaque before the f16 conversion so that the compiler cannot fold
+// the fma or multiply that produced it into one mixed-precision v_fma_mix with
+// an f16 result: that rounds once where the float32 value rounds twice, and the
+// page must hold the float32 value rounded to f16, as the host writes it.
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  asm("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {

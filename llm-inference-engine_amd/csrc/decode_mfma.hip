@@ -85,6 +85,32 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
   return v;
 }
 
+// Folds a page pair's partial (max mj in log2 units, this lane's part lj of the
+// sum of its weights 2^(s - mj), and pv = V^T P^T of those weights) into the
+// running (m, l, o). A side with max -inf saw no position and passes the other
+// side through unchanged; otherwise both are rescaled to the larger max. The
+// same function, in the same pair order, serves one wave folding its pairs and
+// wave 0 folding one pair per wave, so the two layouts give the same bits.
+__device__ __forceinline__ void fold_pair(float& m, float& l, f32x4 (&o)[8], const float mj,
+                                          const float lj, const f32x4 (&pv)[8]) {
+  if (mj == -INFINITY) return;
+  if (m == -INFINITY) {
+    m = mj;
+    l = lj;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) o[mt] = pv[mt];
+    return;
+  }
+  const float mn = fmaxf(m, mj);
+  const float a = exp2_weight(m - mn), b = exp2_weight(mj - mn);
+  m = mn;
+  l = __builtin_fmaf(l, a, lj * b);
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[mt][e] = __builtin_fmaf(o[mt][e], a, pv[mt][e] * b);
+}
+
 // Workgroup `wg` -> (row t, chunk c, position p, sequence seq) in the order
 // "row 0's chunks, row 1's chunks, ...", where row t has min(p / chunk + 1,
 // num_chunks) chunks (none if p < 0). Every wave computes the same answer.
@@ -120,7 +146,7 @@ __device__ __forceinline__ bool locate_chunk(int wg, int T, const int32_t* __res
 // accumulators and the workgroup needs no LDS beyond its V tiles.
 template <int KV, bool kOneWave, bool kFused>
 __global__ void __launch_bounds__(kOneWave ? 64 : 512)
-__attribute__((amdgpu_waves_per_eu(kFused ? 2 : 3)))  // fused: the new row's registers too
+__attribute__((amdgpu_waves_per_eu(2)))  // ~206 registers: a pair partial beside the running one
 decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
                     float* __restrict__ part_ml, const float* __restrict__ q,
                     const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
@@ -155,7 +181,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   // are read from this register (readlane): a scalar load of the table inside
   // the pair loop would share lgkmcnt with the transposed V reads, so the
   // first V wait of every pair would also wait for the table's round trip.
-  // A wave covers at most 32 pages (the host keeps it to 512 positions).
+  // A wave covers at most 64 pages (1,024 positions, the largest chunk).
   const int pi0 = (s0 + wt0) / IE_HIP_PAGE_SIZE;
   const int32_t* row_tab = tables + size_t(seq) * max_pages;
   const int pid_lane = (16 * lane < nw && pi0 + lane < max_pages) ? row_tab[pi0 + lane] : -1;
@@ -374,11 +400,15 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
         sb[i] = (ok_b && tb < nw) ? sb[i] : -INFINITY;
       }
     }
+    // The pair's own partial: its max (per head), weights relative to it, their
+    // sum (this lane's part) and V^T P^T from zero, folded into the running
+    // result by fold_pair. Each pair's partial depends on the pair alone, so a
+    // chunk's result is the same whether one wave folds its pairs as they come
+    // or several waves take one pair each and one of them folds the others'.
     float mx = fmaxf(fmaxf(fmaxf(sa[0], sa[1]), fmaxf(sa[2], sa[3])),
                      fmaxf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3])));
     mx = group_max4(mx);
-    const float m_new = fmaxf(m, mx);
-    const float mref = m_new == -INFINITY ? 0.0f : m_new;  // all masked so far: weights 0
+    const float mref = mx == -INFINITY ? 0.0f : mx;  // nothing visible: weights 0
     op phi, plo;
     float sum = 0.0f;
 #pragma unroll
@@ -393,15 +423,6 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
       plo[i] = la;
       plo[4 + i] = lb;
     }
-    if (j == 0) {
-      l = sum;
-    } else {
-      const float corr = exp2_weight(m - mref);  // m = -inf (nothing seen yet): 0
-      l = __builtin_fmaf(l, corr, sum);
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) o[mt] *= corr;
-    }
-    m = m_new;
 
     // V^T of the pair: two transposing reads per 16-dim tile; in each 16-lane
     // group, lane 4a+b receives element b of the 8-byte reads of lanes a,
@@ -433,6 +454,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
       }
     }
     const unsigned char* vt = warea + (j & 1) * kPair + rtok * 256 + rlo;
+    f32x4 pv[8];
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       const int slot = 2 * (mt ^ rsw) + rpc;
@@ -443,8 +465,32 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
         hi4 = __builtin_bit_cast(s16x4, __builtin_bit_cast(unsigned long long, hi4) & keep_hi);
       }
       const op a = join_tr<op>(lo4, hi4);
-      o[mt] = M::mma(a, phi, o[mt]);
-      o[mt] = M::mma(a, plo, o[mt]);
+      pv[mt] = M::mma(a, phi, f32x4{0.f, 0.f, 0.f, 0.f});
+      pv[mt] = M::mma(a, plo, pv[mt]);
+    }
+    fold_pair(m, l, o, mx, sum, pv);
+  }
+  if constexpr (!kOneWave) {
+    // One pair per wave: waves 1.. hand their pair's partial to wave 0 through
+    // their own LDS area (their V reads are done), and wave 0 folds them in pair
+    // order -- the fold one wave makes over the same pairs.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    if (wave > 0) {
+      f32x4* xo = reinterpret_cast<f32x4*>(warea);
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) xo[mt * 64 + lane] = o[mt];
+      reinterpret_cast<float2*>(warea + kOutTile * 2)[lane] = make_float2(m, l);
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    for (int w = 1; w < waves; ++w) {
+      const unsigned char* wa = smem + size_t(w) * kTile;
+      const float2 ml = reinterpret_cast<const float2*>(wa + kOutTile * 2)[lane];
+      f32x4 ow[8];
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) ow[mt] = reinterpret_cast<const f32x4*>(wa)[mt * 64 + lane];
+      fold_pair(m, l, o, ml.x, ml.y, ow);
     }
   }
   l = group_sum4(l);
@@ -468,44 +514,9 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
       if (d4 == 0) *reinterpret_cast<float2*>(part_ml + 2 * slot) = make_float2(mh * kLn2, lh);
     }
   };
-  if constexpr (kOneWave) {
-    if (head_ok) {
+  if (head_ok) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) emit(r, 4 * j + g, od[j], m, l);
-    }
-  } else {
-    // Waves of the workgroup merged by log-sum-exp through LDS: each wave's
-    // output tile [16 heads][64] and its (m, l) per head in its own area (its V
-    // reads are done).
-    const int waves = blockDim.x >> 6;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    float* ot = reinterpret_cast<float*>(warea);
-    float* st = reinterpret_cast<float*>(warea + kOutTile);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(ot + r * 64 + 16 * j + 4 * g) = od[j];
-    if (g == 0) {
-      st[r] = m;
-      st[16 + r] = l;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < n_heads * 16; idx += blockDim.x) {
-      const int h = idx >> 4, d4 = idx & 15;
-      float mx = -INFINITY;
-      for (int w = 0; w < waves; ++w)
-        mx = fmaxf(mx, reinterpret_cast<const float*>(smem + size_t(w) * kTile + kOutTile)[h]);
-      float lsum = 0.0f;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int w = 0; w < waves; ++w) {
-        const float* sw = reinterpret_cast<const float*>(smem + size_t(w) * kTile + kOutTile);
-        const float sc = sw[h] == -INFINITY ? 0.0f : exp2f(sw[h] - mx);
-        lsum = __builtin_fmaf(sw[16 + h], sc, lsum);
-        acc += *reinterpret_cast<const f32x4*>(
-                   reinterpret_cast<const float*>(smem + size_t(w) * kTile) + h * 64 + 4 * d4) *
-               sc;
-      }
-      emit(h, d4, acc, mx, lsum);
-    }
+    for (int j = 0; j < 4; ++j) emit(r, 4 * j + g, od[j], m, l);
   }
 }
 
@@ -705,15 +716,17 @@ bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_d
          chunk_tokens <= 1024;
 }
 
-// Waves per workgroup for a chunk: one per 128 positions (at most 8, a whole
-// number of page pairs each). A wave streams its positions as page pairs, one
-// pair in flight while it computes the previous one. The split depends on the
-// chunk size alone, never on the grid: the waves' results are merged in a
-// fixed order, so a row's output is the same whatever batch it is in.
-static int decode_mfma_waves(int chunk_tokens) {
-  int w = std::max(1, std::min(kMaxWaves, chunk_tokens / 128));
-  while (w > 1 && chunk_tokens % (32 * w) != 0) --w;
-  return w;
+// Waves per workgroup for a chunk. One wave streams the chunk as page pairs,
+// one pair in flight while it computes the previous one: that hides latency
+// when the grid is large. When the grid gives fewer than two workgroups per
+// compute unit (few, long rows), a chunk of 2 to 8 pairs takes one wave per
+// pair instead, every pair in flight at once. Either way the pairs' partials
+// are folded in pair order by the same function (fold_pair), so the choice
+// changes the timing and never the result.
+static int decode_mfma_waves(int chunk_tokens, int64_t slots) {
+  const bool small_grid = slots < 2 * int64_t(device_compute_units());
+  if (small_grid && chunk_tokens >= 64 && chunk_tokens <= 32 * kMaxWaves) return chunk_tokens / 32;
+  return 1;
 }
 
 int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
@@ -722,10 +735,10 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
                 hipStream_t stream, const FusedAppend* fused) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
   const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
-  const int waves = decode_mfma_waves(chunk_tokens);
+  const int waves = decode_mfma_waves(chunk_tokens, slots);
   const size_t lds = size_t(waves) * kTile;
-  if (chunk_tokens / waves > 512)  // a wave's page ids live one per lane
-    return fail(IE_HIP_EINVAL, "attention: more than 512 positions per wave");
+  if (chunk_tokens / waves > 1024)  // a wave's page ids live one per lane
+    return fail(IE_HIP_EINVAL, "attention: more than 1,024 positions per wave");
   if (slots * n_heads * 64 * 4 > 0x7fffffff)
     return fail(IE_HIP_EINVAL, "attention: split-K workspace above 2 GB (too many rows x chunks)");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |

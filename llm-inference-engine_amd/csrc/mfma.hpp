@@ -114,9 +114,15 @@ __device__ __forceinline__ Op join_tr(s16x4 lo, s16x4 hi) {
 
 // x = hi + lo in the 16-bit type E, |x - hi - lo| ~ 2^-22 |x|. x - hi is exact in
 // float32; written as an fma of the widened hi so that for f16 it becomes one
-// mixed-precision v_fma_mix (f32 and f16 sources, f16 result).
+// mixed-precision v_fma_mix (f32 and f16 sources, f16 result). x is made opaque
+// first: otherwise, when x is a product, the compiler may fold the multiply into
+// the conversion (v_fma_mixlo_f16 a, b, 0), rounding the exact product once to
+// f16 instead of the float32 product to f16 -- one ulp apart in rare cases, and
+// chosen differently in different kernels, so two paths over the same data
+// would not give the same bits.
 template <typename E>
 __device__ __forceinline__ void split16(float x, E& hi, E& lo) {
+  asm("" : "+v"(x));
   hi = static_cast<E>(x);
   lo = static_cast<E>(__builtin_fmaf(-1.0f, static_cast<float>(hi), x));
 }
