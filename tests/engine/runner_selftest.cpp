@@ -26,9 +26,18 @@
 //           bit for bit, through two engines;
 //   serve   the continuous-batching scheduler (include/ie_hip_serve.hpp): 24
 //           requests at concurrency 1, 4 and 16 give identical tokens
-//           (serve-bench --check, src/main.cpp:845-888).
+//           (serve-bench --check, src/main.cpp:845-888);
+//   checkpoint (with --checkpoint DIR, instead of the sections above) a model
+//           directory on disk (config.json + model.safetensors, written by
+//           tests/checkpoint.py) read by the reference's own loader --
+//           load_config (src/config.cpp), SafeTensorsFile (src/safetensors.cpp),
+//           load_weights (src/weights.cpp:89-117) -- as BF16 and as INT8, the
+//           way the reference's CLI loads a model (src/main.cpp:314-325), then
+//           served by make_batch_runner and by the CPU Runner from the same
+//           Weights: prompt and decode logits, untied LM head, q/k/v biases.
 //
-// usage: runner_selftest f32|f16|bf16 [bf16|int8]   exit status 0 when every check passes.
+// usage: runner_selftest f32|f16|bf16 [bf16|int8] [--checkpoint DIR]
+// exit status 0 when every check passes.
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -40,7 +49,10 @@
 
 #include "ie_hip_runner.hpp"
 #include "ie_hip_serve.hpp"
-#include "runner.h"  // reference: src/runner.h
+#include "config.h"       // reference: src/config.h (load_config)
+#include "runner.h"       // reference: src/runner.h
+#include "safetensors.h"  // reference: src/safetensors.h
+#include "weights.h"      // reference: src/weights.h (load_weights)
 
 namespace {
 
@@ -402,11 +414,56 @@ void section_serve(Ctx& c) {
   }
 }
 
+
+void section_checkpoint(Ctx& c, const std::string& dir) {
+  std::printf("---- checkpoint %s\n", dir.c_str());
+  const ie::Config cfg = ie::load_config(dir + "/config.json");
+  const ie::SafeTensorsFile st(dir + "/model.safetensors");
+  result(cfg.num_layers == 2 && cfg.head_dim == 64 && !cfg.tie_word_embeddings &&
+             st.contains("lm_head.weight") && st.contains("model.layers.1.self_attn.q_proj.bias"),
+         "config.json and the safetensors index read by the reference's loader");
+  for (const ie::DType dt : {ie::DType::BF16, ie::DType::I8}) {
+    const std::string dn = dt == ie::DType::BF16 ? "bf16" : "int8";
+    const ie::Weights w = ie::load_weights(st, cfg, dt);
+    std::unique_ptr<ie::BatchRunner> gpu =
+        ie::hip::make_batch_runner(cfg, w, 2, 256, size_t(64) << 20, true, c.kv);
+    std::unique_ptr<ie::Runner> cpu = ie::make_cpu_runner(cfg, w, 256);
+    result(gpu->weight_bytes() == w.matrix_bytes() && gpu->config().vocab_size == cfg.vocab_size,
+           dn + ": weight_bytes and config of the served model");
+    std::uniform_int_distribution<int> d(0, cfg.vocab_size - 1);
+    std::vector<int32_t> prompt(29);
+    for (auto& e : prompt) e = d(c.rng);
+    const int s = gpu->open_sequence();
+    const std::vector<float> gp = gpu->prefill(s, prompt), cp = cpu->forward(prompt);
+    double worst = rel_err(gp, cp);
+    // Decode follows the CPU's greedy tokens, so both see the same sequence
+    // whatever a near-tie does; the GPU's own greedy choice is counted.
+    int32_t tok = host_argmax(cp.data(), cfg.vocab_size);
+    int agree = 0;
+    const int steps = 6;
+    for (int i = 0; i < steps; ++i) {
+      const std::vector<float> g = gpu->decode({s}, {tok}), r = cpu->forward({tok});
+      worst = std::max(worst, rel_err(g, r));
+      const int32_t rt = host_argmax(r.data(), cfg.vocab_size);
+      agree += host_argmax(g.data(), cfg.vocab_size) == rt;
+      tok = rt;
+    }
+    char b[200];
+    std::snprintf(b, sizeof(b), "%s: prefill of 29 tokens and %d decode steps, logits rel %.2e "
+                  "(greedy agrees on %d of %d)", dn.c_str(), steps, worst, agree, steps);
+    result(worst <= c.tol, b);
+    result(gpu->sequence_length(s) == 29 + steps, dn + ": sequence length after decode");
+    gpu->close_sequence(s);
+    result(gpu->free_pages() == gpu->total_pages(), dn + ": pages returned on close");
+  }
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
   const std::string kvs = argc > 1 ? argv[1] : "f32";
   const std::string wts = argc > 2 ? argv[2] : "bf16";
+  const std::string ckpt = argc > 4 && std::string(argv[3]) == "--checkpoint" ? argv[4] : "";
   std::printf("runner self-test: %s KV cache, %s weights, device %s\n", kvs.c_str(), wts.c_str(),
               ie::hip::device_description().c_str());
   std::fflush(stdout);
@@ -420,11 +477,15 @@ int main(int argc, char** argv) {
     c.kv = kvs == "f16" ? ie::hip::KvDtype::F16
                         : kvs == "bf16" ? ie::hip::KvDtype::BF16 : ie::hip::KvDtype::F32;
     c.tol = c.kv == ie::hip::KvDtype::F32 ? 1e-5 : 1e-2;
-    c.w = random_weights(c.cfg, wts == "int8" ? ie::DType::I8 : ie::DType::BF16, 7u);
-    section_batch(c);
-    section_runner(c);
-    section_invariance(c);
-    section_serve(c);
+    if (!ckpt.empty()) {
+      section_checkpoint(c, ckpt);
+    } else {
+      c.w = random_weights(c.cfg, wts == "int8" ? ie::DType::I8 : ie::DType::BF16, 7u);
+      section_batch(c);
+      section_runner(c);
+      section_invariance(c);
+      section_serve(c);
+    }
   } catch (const std::exception& e) {
     std::printf("FAIL exception: %s\n", e.what());
     return 2;

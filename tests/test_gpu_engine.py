@@ -97,3 +97,48 @@ def test_runner_selftest(kv, weights):
     fails = [l for l in r.stdout.splitlines() if l.startswith("FAIL")]
     assert r.returncode == 0 and not fails, "\n".join(fails) or f"exit status {r.returncode}"
     assert " checks, 0 failures" in r.stdout
+
+
+def test_checkpoint_writer_round_trip(tmp_path):
+    """CPU: the checkpoint the GPU test serves (tests/checkpoint.py) is a valid
+    safetensors file -- read back by the safetensors package, an independent reader,
+    every tensor's BF16 bits equal torch's round-to-nearest-even of the float32
+    weights -- and config.json has the keys the reference's load_config reads
+    (src/config.cpp:16-26)."""
+    import json
+    import torch
+    from safetensors.torch import load_file
+    from checkpoint import write_checkpoint
+    want = write_checkpoint(str(tmp_path), seed=5, layers=1, inter=64, vocab=32, tie=False)
+    got = load_file(str(tmp_path / "model.safetensors"))
+    assert sorted(got) == sorted(want)
+    for name, x in want.items():
+        ref = torch.from_numpy(x).to(torch.bfloat16)
+        assert got[name].dtype == torch.bfloat16 and tuple(got[name].shape) == x.shape, name
+        assert torch.equal(got[name].view(torch.int16), ref.view(torch.int16)), name
+    cfg = json.load(open(tmp_path / "config.json"))
+    for key in ("hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+                "num_key_value_heads", "vocab_size", "rms_norm_eps", "rope_theta",
+                "tie_word_embeddings"):
+        assert key in cfg, key
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_runner_checkpoint(tmp_path, kv):
+    """safetensors -> device weights through the drop-in: a 2-layer checkpoint on disk
+    (untied LM head, q/k/v biases) read by the reference's own loader (load_config,
+    SafeTensorsFile, load_weights as BF16 and INT8), served by make_batch_runner and
+    by the reference's CPU Runner from the same Weights; prompt and decode logits
+    agree within the runner self-test's tolerance."""
+    if not os.path.exists(RUNNER_BIN):
+        pytest.skip("runner_selftest not built (no reference checkout where the tree was built)")
+    from checkpoint import write_checkpoint
+    write_checkpoint(str(tmp_path))
+    print(f"runner_selftest {kv} --checkpoint {tmp_path}", flush=True)
+    r = subprocess.run([RUNNER_BIN, kv, "bf16", "--checkpoint", str(tmp_path)],
+                       capture_output=True, text=True, timeout=200)
+    print(r.stdout[-8000:], r.stderr[-2000:], flush=True)
+    fails = [l for l in r.stdout.splitlines() if l.startswith("FAIL")]
+    assert r.returncode == 0 and not fails, "\n".join(fails) or f"exit status {r.returncode}"
+    assert " checks, 0 failures" in r.stdout and "---- checkpoint" in r.stdout
