@@ -471,7 +471,8 @@ def bench_append(args, torch, ie, O):
         v = torch.randn((rows, KVD), generator=gen, device=dev)
         if rows == 64:
             cpu_in = (q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), pos.copy())
-        for with_q in (False, True):
+        modes = {"off": (False,), "on": (True,), "both": (False, True)}[args.append_q]
+        for with_q in modes:
             def step(i):
                 ie.rope_and_cache(q if with_q else None, k, v, k_pool, v_pool, table, d_pos, d_seq,
                                   d_tab, max_pages, NH, NKV, HD)
@@ -479,7 +480,7 @@ def bench_append(args, torch, ie, O):
             per_row = (1024 + 2 * KVD * KV_BYTES[kv] + 8 + 4) + (2 * QD * 4 if with_q else 0)
             sweep.append({"rows": rows, "with_q": with_q, "us_per_launch": round(ms * 1e3, 3),
                           "gbs": round(rows * per_row / (ms * 1e-3) / 1e9, 2)})
-    head = [s for s in sweep if s["rows"] == 64 and not s["with_q"]][0]
+    head = [s for s in sweep if s["rows"] == 64 and s["with_q"] == (args.append_q == "on")][0]
     res = {
         "metric": "paged RoPE+KV append GB/s at batch 64 (K/V only), 1 GPU",
         "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -774,7 +775,7 @@ def extra_targets(args, torch, ie, O):
     sub = copy.copy(args)
     sub.no_cpu, sub.kv, sub.chunk_tokens, sub.sweep = True, None, None, False
     sub.steps, sub.warmup = max(20, min(args.steps, 100)), 5
-    sub.append_rows = [64, 131072]
+    sub.append_rows, sub.append_q = [64, 131072], "off"
     app = bench_append(sub, torch, ie, O)
     pts = {s["rows"]: s for s in app["sweep"] if not s["with_q"]}
     mix = bench_mixed(sub, torch, ie, O)
@@ -1073,6 +1074,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true", help="config 2: rows-per-launch sweep")
+    ap.add_argument("--append-q", choices=["off", "on", "both"], default="both",
+                    help="config 2: time the append without q (K/V only), with q rotated in "
+                         "place, or both (the headline is K/V only unless 'on'); one mode "
+                         "alone gives per-dispatch counters of that mode")
     ap.add_argument("--probe", action="store_true", help="also measure device copy bandwidth")
     ap.add_argument("--no-probe", action="store_true",
                     help="config 3: skip the HBM read probes (ceiling_gbs)")
