@@ -382,11 +382,24 @@ def bench_decode(args, torch, ie, O):
     nc = ie.attention_chunks(4096, ct)
     ws = ie.attention_workspace(B, NH, HD, nc)
     stream = torch.cuda.current_stream()
+    # The work list the engine builds on the host for a decode step (the rows'
+    # positions and sequences and the block table are host data there): one
+    # dependent load before the first K/V byte instead of three. The positions are
+    # fixed across steps here, so it is built and copied once.
+    d_plan = None
+    if args.plan == "on":
+        d_plan = torch.from_numpy(ie.attention_plan((lens - 1).astype(np.int32),
+                                                    np.arange(B, dtype=np.int32), tables, nc,
+                                                    ct)).to(dev)
 
     def step(i):
         l = i % args.layers
-        ie.attention(out, q, k_pools[l], v_pools[l], d_pos, d_seq, d_tab, max_pages, nc, ct, ws,
-                     NH, NKV, HD)
+        if d_plan is not None:
+            ie.attention_planned(out, q, k_pools[l], v_pools[l], d_pos, d_seq, d_tab, max_pages,
+                                 nc, ct, ws, d_plan, NH, NKV, HD)
+        else:
+            ie.attention(out, q, k_pools[l], v_pools[l], d_pos, d_seq, d_tab, max_pages, nc, ct,
+                         ws, NH, NKV, HD)
 
     ms = time_steps(torch, step, args.steps, args.warmup, stream)
     timing = dict(TIMING)
@@ -410,7 +423,9 @@ def bench_decode(args, torch, ie, O):
                                f"65,536-page pools, {ct}-token split-K + LSE merge",
                    "kv_dtype": kv, "batch": B, "chunk_tokens": ct, "num_chunks": nc,
                    "layers_rotated": args.layers, "seed": args.seed,
-                   "context_tokens": int(lens.sum())},
+                   "context_tokens": int(lens.sum()),
+                   "work_list": "host-built (ie_hip_attention_plan)" if d_plan is not None
+                   else "located on the device"},
         "attn_tok_per_s": round(B / (ms * 1e-3), 1),
         "context_tok_per_s": round(float(lens.sum()) / (ms * 1e-3), 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -418,7 +433,8 @@ def bench_decode(args, torch, ie, O):
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles("decode", kv, "f16", args),
                      "kernel": ("decode_partial_mfma_f32" if kv == "f32" else "decode_partial_mfma")
-                               + " + decode_merge_kernel (one ie_hip_attention call)",
+                               + " + decode_merge_kernel (one ie_hip_attention"
+                               + ("_planned" if d_plan is not None else "") + " call)",
                      "us_per_launch": round(ms * 1e3, 3)},
         "algorithmic_bytes_per_step": nbytes,
         "timing": timing,
@@ -532,17 +548,33 @@ def bench_long(args, torch, ie, O):
     # The layer's RoPE + append and attention in one launch where the library offers it
     # (16-bit caches at the matrix-core kernel's shapes), else the two calls.
     fused = not args.unfused and ie.rope_cache_attention_supported(KV_CODES[kv], NH, NKV, HD, ct)
+    # Host-built work lists, one per layer (each layer's table differs), as the engine
+    # builds them for a decode step.
+    plans = None
+    if args.plan == "on":
+        plans = [torch.from_numpy(ie.attention_plan(np.array([L - 1], np.int32),
+                                                    np.zeros(1, np.int32), tabs[l].cpu().numpy(),
+                                                    nc, ct)).to(dev) for l in range(layers)]
 
     def step(i):
         for l in range(layers):
+            if fused and plans is not None:
+                ie.rope_cache_attention_planned(out, q[l], k[l], v[l], k_pools[l], v_pools[l],
+                                                table, d_pos, d_seq, tabs[l], pages, nc, ct, ws,
+                                                plans[l], NH, NKV, HD)
+                continue
             if fused:
                 ie.rope_cache_attention(out, q[l], k[l], v[l], k_pools[l], v_pools[l], table,
                                         d_pos, d_seq, tabs[l], pages, nc, ct, ws, NH, NKV, HD)
                 continue
             ie.rope_and_cache(q[l], k[l], v[l], k_pools[l], v_pools[l], table, d_pos, d_seq,
                               tabs[l], pages, NH, NKV, HD)
-            ie.attention(out, q[l], k_pools[l], v_pools[l], d_pos, d_seq, tabs[l], pages, nc, ct,
-                         ws, NH, NKV, HD)
+            if plans is not None:
+                ie.attention_planned(out, q[l], k_pools[l], v_pools[l], d_pos, d_seq, tabs[l],
+                                     pages, nc, ct, ws, plans[l], NH, NKV, HD)
+            else:
+                ie.attention(out, q[l], k_pools[l], v_pools[l], d_pos, d_seq, tabs[l], pages, nc,
+                             ct, ws, NH, NKV, HD)
 
     ms = time_steps(torch, step, args.steps, args.warmup, stream)
     per_layer = 2 * KVD * KV_BYTES[kv] * L + 2 * QD * 4 + 4 * pages + 8 + \
@@ -557,8 +589,11 @@ def bench_long(args, torch, ie, O):
         "config": {"workload": "config 4: 24 layers x (RoPE+append at 32,767, flash-decoding "
                                "over 32,768 positions), batch 1, shuffled 16-token pages",
                    "kv_dtype": kv, "chunk_tokens": ct, "num_chunks": nc, "seed": args.seed,
-                   "layer_calls": "rope_cache_attention" if fused
-                   else "rope_and_cache + attention"},
+                   "layer_calls": ("rope_cache_attention" if fused
+                                   else "rope_and_cache + attention")
+                   + ("_planned" if plans is not None else ""),
+                   "work_list": "host-built (ie_hip_attention_plan)" if plans is not None
+                   else "located on the device"},
         "tok_per_s": round(1 / (ms * 1e-3), 1), "us_per_layer": round(ms * 1e3 / layers, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -1074,6 +1109,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true", help="config 2: rows-per-launch sweep")
+    ap.add_argument("--plan", choices=["on", "off"], default="on",
+                    help="configs 3 and 4: the decode work list built on the host "
+                         "(ie_hip_attention_plan), as the engine does, or located by the kernel")
     ap.add_argument("--append-q", choices=["off", "on", "both"], default="both",
                     help="config 2: time the append without q (K/V only), with q rotated in "
                          "place, or both (the headline is K/V only unless 'on'); one mode "

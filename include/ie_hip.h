@@ -151,6 +151,39 @@ int ie_hip_attention_noalloc(float* out, const float* q, const void* k_pool, con
                              ie_kv_layout kv, int num_chunks, int chunk_tokens, int n_heads,
                              int n_kv_heads, int head_dim, hipStream_t stream);
 
+/* -------------------------------------------- host-planned decode work ---
+ * The decode kernel's work list built on the host, from host copies of the
+ * rows' positions and sequences and of the block table -- what the reference's
+ * engine holds on the host anyway (CudaEngine::run stages rows_pos/rows_seq
+ * and the page tables there, src/cuda/cuda_runner.cu:366-381) -- so the 16-bit
+ * kernel reaches its first K/V load after one dependent load (its item: row,
+ * chunk, position, sequence, the chunk's page ids) instead of three (row
+ * positions, then the row's table, then K/V). No counterpart in the reference:
+ * its attention_partial_kernel reads the table itself (kernels.cu:367-371).
+ * Results are bit-identical to the unplanned calls.
+ *
+ * ie_hip_attention_plan_ints: int32 capacity of a plan for a launch of T rows
+ * and num_chunks chunks of chunk_tokens (0 for invalid arguments).
+ * ie_hip_attention_plan: writes the plan to HOST memory `plan` (capacity
+ * plan_capacity ints) from host row_pos / row_seq [T] and the host table
+ * [max_seqs * max_pages]; pages past a row's position or its table row are
+ * -1, and ids outside the pool are left for the kernel to skip. Copy it to the
+ * device (16-byte aligned) before the launch that uses it; it must describe
+ * that launch's rows, positions, chunk_tokens and num_chunks.
+ * ie_hip_attention_planned / ie_hip_rope_cache_attention_planned: as
+ * ie_hip_attention / ie_hip_rope_cache_attention with the device copy of the
+ * plan. row_pos still goes to the merge; tables still serve the other kernels
+ * (f32 and VALU caches ignore the plan) and the fused append's page slot. */
+size_t ie_hip_attention_plan_ints(int T, int num_chunks, int chunk_tokens);
+int ie_hip_attention_plan(int32_t* plan, size_t plan_capacity, int T, const int32_t* row_pos,
+                          const int32_t* row_seq, const int32_t* tables, int max_seqs,
+                          int max_pages, int num_chunks, int chunk_tokens);
+int ie_hip_attention_planned(float* out, const float* q, const void* k_pool, const void* v_pool,
+                             int T, const int32_t* row_pos, const int32_t* row_seq,
+                             ie_kv_layout kv, int num_chunks, int chunk_tokens, void* workspace,
+                             const int32_t* plan, size_t plan_capacity, int n_heads,
+                             int n_kv_heads, int head_dim, hipStream_t stream);
+
 /* ------------------------------------------ decode step in one launch ---
  * ie_hip_rope_and_cache followed by ie_hip_attention, in one launch: the
  * reference's per-layer decode sequence rope_and_cache + attention
@@ -172,6 +205,14 @@ int ie_hip_rope_cache_attention(float* out, const float* q, const float* k, cons
                                 const int32_t* row_seq, ie_kv_layout kv, int num_chunks,
                                 int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
                                 int head_dim, hipStream_t stream);
+int ie_hip_rope_cache_attention_planned(float* out, const float* q, const float* k,
+                                        const float* v, void* k_pool, void* v_pool,
+                                        const float* rope_table, int table_positions, int T,
+                                        const int32_t* row_pos, const int32_t* row_seq,
+                                        ie_kv_layout kv, int num_chunks, int chunk_tokens,
+                                        void* workspace, const int32_t* plan,
+                                        size_t plan_capacity, int n_heads, int n_kv_heads,
+                                        int head_dim, hipStream_t stream);
 
 /* --------------------------------------------------- prefill attention ---
  * Attention for T rows that are consecutive positions of ONE sequence

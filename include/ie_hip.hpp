@@ -59,6 +59,27 @@ inline void attention(float* out, const float* q, const void* k_pool, const void
                          chunk_tokens, workspace, n_heads, n_kv_heads, head_dim, stream));
 }
 
+/* The decode work list built on the host (ie_hip_attention_plan) and the calls
+ * that read it; results are those of attention / rope_cache_attention. */
+inline size_t attention_plan_ints(int T, int num_chunks, int chunk_tokens) {
+  return ie_hip_attention_plan_ints(T, num_chunks, chunk_tokens);
+}
+inline void attention_plan(int32_t* plan, size_t plan_capacity, int T, const int* row_pos,
+                           const int* row_seq, const int32_t* tables, int max_seqs, int max_pages,
+                           int num_chunks, int chunk_tokens) {
+  check(ie_hip_attention_plan(plan, plan_capacity, T, row_pos, row_seq, tables, max_seqs,
+                              max_pages, num_chunks, chunk_tokens));
+}
+inline void attention_planned(float* out, const float* q, const void* k_pool, const void* v_pool,
+                              int T, const int* row_pos, const int* row_seq, const KvLayout& kv,
+                              int num_chunks, int chunk_tokens, void* workspace,
+                              const int32_t* plan, size_t plan_capacity, int n_heads,
+                              int n_kv_heads, int head_dim, hipStream_t stream) {
+  check(ie_hip_attention_planned(out, q, k_pool, v_pool, T, row_pos, row_seq, kv.c(), num_chunks,
+                                 chunk_tokens, workspace, plan, plan_capacity, n_heads,
+                                 n_kv_heads, head_dim, stream));
+}
+
 /* rope_and_cache followed by attention for a decode step, in one launch
  * (rows of distinct sequences; see ie_hip_rope_cache_attention). */
 inline bool rope_cache_attention_supported(int kv_dtype, int n_heads, int n_kv_heads,
@@ -75,6 +96,20 @@ inline void rope_cache_attention(float* out, const float* q, const float* k, con
   check(ie_hip_rope_cache_attention(out, q, k, v, k_pool, v_pool, rope_table, table_positions, T,
                                     row_pos, row_seq, kv.c(), num_chunks, chunk_tokens, workspace,
                                     n_heads, n_kv_heads, head_dim, stream));
+}
+
+inline void rope_cache_attention_planned(float* out, const float* q, const float* k,
+                                         const float* v, void* k_pool, void* v_pool,
+                                         const float* rope_table, int table_positions, int T,
+                                         const int* row_pos, const int* row_seq,
+                                         const KvLayout& kv, int num_chunks, int chunk_tokens,
+                                         void* workspace, const int32_t* plan,
+                                         size_t plan_capacity, int n_heads, int n_kv_heads,
+                                         int head_dim, hipStream_t stream) {
+  check(ie_hip_rope_cache_attention_planned(out, q, k, v, k_pool, v_pool, rope_table,
+                                            table_positions, T, row_pos, row_seq, kv.c(),
+                                            num_chunks, chunk_tokens, workspace, plan,
+                                            plan_capacity, n_heads, n_kv_heads, head_dim, stream));
 }
 
 /* attention_prefill_supported / attention_prefill (kernels.cuh:89-96). */

@@ -84,6 +84,7 @@ struct StepInfo {
   bool graph = false;   // replayed a decode graph
   bool prompt = false;  // prefill attention (rows: consecutive positions of one sequence)
   bool fused = false;   // RoPE + append + attention in one launch per layer
+  bool planned = false; // flash-decoding read a host-built work list (ie_hip_attention_plan)
   int chunk_tokens = 0, chunks = 0;  // flash-decoding partition (0 for a prompt)
 };
 
@@ -179,6 +180,13 @@ class KvEngine {
     chunk_tokens_ = attention_chunk_tokens(lim_.max_batch, lim_.max_seq_len, kv_dtype_);
     max_chunks_ = attention_chunks(lim_.max_seq_len, chunk_tokens_);
     attn_rows_ = std::max(lim_.max_batch, kPromptMinRows);  // rows per flash-decoding launch
+    // A step of up to attn_rows_ flash-decoding rows sends, with its inputs, the
+    // work list the 16-bit kernel would otherwise locate on the device (row
+    // positions -> the row's table -> K/V): built here from host data, it cuts
+    // that chain to one load.
+    plan_ints_ = kv_dtype_ == IE_KV_F32
+                     ? 0
+                     : attention_plan_ints(attn_rows_, max_chunks_, chunk_tokens_);
 
     pages_ = ie_pages_create(lim_.num_pages, lim_.max_batch, lim_.max_seq_len);
     if (!pages_) throw std::runtime_error(ie_hip_last_error());
@@ -308,8 +316,9 @@ class KvEngine {
                                                            chunk_tokens_);
     }
 
-    // Inputs: [seq T][pos T][ids T][logit rows R], one copy. The offsets depend
-    // only on T, so a decode graph (one per T and R) reads them where it recorded.
+    // Inputs: [seq T][pos T][ids T][logit rows R][work list], one copy. The
+    // offsets depend only on T and R, so a decode graph (one per T and R) reads
+    // them where it recorded.
     check(hipEventSynchronize(staged_), "staging");  // the previous step's copy is done
     int32_t* h = staging_.as<int32_t>();
     std::copy(seq.begin(), seq.end(), h);
@@ -319,8 +328,16 @@ class KvEngine {
     else
       std::copy(ids.begin(), ids.end(), h + 2 * T);
     std::copy(logit_rows.begin(), logit_rows.end(), h + 3 * T);
-    check(hipMemcpyAsync(inputs_, h, sizeof(int32_t) * (3 * size_t(T) + R), hipMemcpyHostToDevice,
-                         stream_),
+    size_t n_in = 3 * size_t(T) + R;
+    s.planned = !s.prompt && plan_ints_ > 0 && T <= attn_rows_;
+    if (s.planned) {
+      const size_t off = plan_offset(T, R);
+      attention_plan(h + off, plan_ints_, T, pos.data(), seq.data(),
+                     ie_pages_host_tables(pages_), lim_.max_batch, max_pages_per_seq_, s.chunks,
+                     s.chunk_tokens);
+      n_in = off + 4 + size_t(h[off]) * ((plan_ints_ - 4) / (size_t(attn_rows_) * max_chunks_));
+    }
+    check(hipMemcpyAsync(inputs_, h, sizeof(int32_t) * n_in, hipMemcpyHostToDevice, stream_),
           "step inputs");
     check(hipEventRecord(staged_, stream_), "hipEventRecord");
     check(ie_pages_upload_tables(pages_, tables_, stream_, nullptr));  // only after page changes
@@ -402,7 +419,11 @@ class KvEngine {
   }
 
  private:
-  size_t input_ints() const { return 3 * size_t(lim_.step_rows) + size_t(lim_.logit_rows); }
+  /* The step's inputs, then (16-byte aligned) the work list of a planned step. */
+  static size_t plan_offset(int T, int R) { return (3 * size_t(T) + size_t(R) + 3) & ~size_t(3); }
+  size_t input_ints() const {
+    return plan_offset(lim_.step_rows, lim_.logit_rows) + plan_ints_;
+  }
 
   static bool distinct_sequences(const std::vector<int>& seq) {
     std::vector<int> s(seq);
@@ -441,7 +462,12 @@ class KvEngine {
       if (body_.before_attention) body_.before_attention(l, T, stream_);
       void* kp = k_pool(l);
       void* vp = v_pool(l);
-      if (s.fused) {
+      const int32_t* plan = inputs_ + plan_offset(T, s.logit_rows);
+      if (s.fused && s.planned) {
+        rope_cache_attention_planned(attn_, q_, k_, v_, kp, vp, rope_, lim_.max_seq_len, T, rpos,
+                                     rseq, kv, s.chunks, s.chunk_tokens, workspace_, plan,
+                                     plan_ints_, NH, NKV, HD, stream_);
+      } else if (s.fused) {
         for (int r0 = 0; r0 < T; r0 += attn_rows_) {
           const int n = std::min(attn_rows_, T - r0);
           rope_cache_attention(attn_ + size_t(r0) * cfg_.q_dim(), q_ + size_t(r0) * cfg_.q_dim(),
@@ -454,6 +480,9 @@ class KvEngine {
                        HD, stream_);
         if (s.prompt) {
           attention_prefill(attn_, q_, kp, vp, T, rpos, rseq, kv, NH, NKV, HD, stream_);
+        } else if (s.planned) {
+          attention_planned(attn_, q_, kp, vp, T, rpos, rseq, kv, s.chunks, s.chunk_tokens,
+                            workspace_, plan, plan_ints_, NH, NKV, HD, stream_);
         } else {
           for (int r0 = 0; r0 < T; r0 += attn_rows_) {
             const int n = std::min(attn_rows_, T - r0);
@@ -511,6 +540,7 @@ class KvEngine {
   LayerBody body_;
   std::string name_;
   int chunk_tokens_ = 0, max_chunks_ = 0, attn_rows_ = 0, max_pages_per_seq_ = 0;
+  size_t plan_ints_ = 0;  // capacity of a step's work list (0: f32 caches, no plan)
 
   ie_page_pool* pages_ = nullptr;  // free list, sequences, host page table
   DeviceArena arena_;

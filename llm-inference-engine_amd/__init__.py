@@ -66,6 +66,13 @@ _SIGS = {
                               _vp]),
     "ie_hip_attention_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _i, _i,
                                       _i, _vp]),
+    "ie_hip_attention_plan_ints": (ctypes.c_size_t, [_i, _i, _i]),
+    "ie_hip_attention_plan": (_i, [_vp, ctypes.c_size_t, _i, _vp, _vp, _vp, _i, _i, _i, _i]),
+    "ie_hip_attention_planned": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _vp, _vp,
+                                      ctypes.c_size_t, _i, _i, _i, _vp]),
+    "ie_hip_rope_cache_attention_planned": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp,
+                                                 _vp, KvLayout, _i, _i, _vp, _vp, ctypes.c_size_t,
+                                                 _i, _i, _i, _vp]),
     "ie_hip_rope_cache_attention_supported": (_i, [_i, _i, _i, _i, _i]),
     "ie_hip_rope_cache_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp,
                                          KvLayout, _i, _i, _vp, _i, _i, _i, _vp]),
@@ -221,6 +228,57 @@ def attention_noalloc(out, q, k_pool, v_pool, row_pos, row_seq, tables, max_page
                                           _ptr(row_pos), _ptr(row_seq), kv, num_chunks,
                                           chunk_tokens, n_heads, n_kv_heads, head_dim,
                                           _stream(stream)))
+
+
+def attention_plan_ints(T: int, num_chunks: int, chunk_tokens: int) -> int:
+    return int(lib().ie_hip_attention_plan_ints(T, num_chunks, chunk_tokens))
+
+
+def attention_plan(row_pos, row_seq, tables, num_chunks: int, chunk_tokens: int):
+    """The decode work list for one launch, built on the host from host copies (numpy
+    int32) of the rows' positions and sequences and of the block table [seqs, max_pages];
+    returns it as a numpy int32 array (copy it to the device for attention_planned)."""
+    import numpy as np
+    row_pos = np.ascontiguousarray(row_pos, dtype=np.int32)
+    row_seq = np.ascontiguousarray(row_seq, dtype=np.int32)
+    tables = np.ascontiguousarray(tables, dtype=np.int32)
+    T = row_pos.size
+    n = int(lib().ie_hip_attention_plan_ints(max(T, 1), num_chunks, chunk_tokens))
+    if n == 0:
+        raise IeHipError(EINVAL, "attention_plan: bad chunk arguments")
+    plan = np.zeros(n, np.int32)
+    _check(lib().ie_hip_attention_plan(plan.ctypes.data, n, T, row_pos.ctypes.data,
+                                       row_seq.ctypes.data, tables.ctypes.data, tables.shape[0],
+                                       tables.shape[1], num_chunks, chunk_tokens))
+    return plan
+
+
+def attention_planned(out, q, k_pool, v_pool, row_pos, row_seq, tables, max_pages: int,
+                      num_chunks: int, chunk_tokens: int, workspace, plan, n_heads: int,
+                      n_kv_heads: int, head_dim: int, stream=None) -> None:
+    """attention() with a device copy of attention_plan()'s work list."""
+    T = row_pos.numel()
+    kv = layout(tables, max_pages, k_pool.numel() // (PAGE_SIZE * n_kv_heads * head_dim),
+                _dtype_code(k_pool))
+    _check(lib().ie_hip_attention_planned(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), T,
+                                          _ptr(row_pos), _ptr(row_seq), kv, num_chunks,
+                                          chunk_tokens, _ptr(workspace), _ptr(plan), plan.numel(),
+                                          n_heads, n_kv_heads, head_dim, _stream(stream)))
+
+
+def rope_cache_attention_planned(out, q, k, v, k_pool, v_pool, table, row_pos, row_seq, tables,
+                                 max_pages: int, num_chunks: int, chunk_tokens: int, workspace,
+                                 plan, n_heads: int, n_kv_heads: int, head_dim: int,
+                                 stream=None) -> None:
+    """rope_cache_attention() with a device copy of attention_plan()'s work list."""
+    T = row_pos.numel()
+    kv = layout(tables, max_pages, k_pool.numel() // (PAGE_SIZE * n_kv_heads * head_dim),
+                _dtype_code(k_pool))
+    _check(lib().ie_hip_rope_cache_attention_planned(
+        _ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(k_pool), _ptr(v_pool), _ptr(table),
+        table.shape[0], T, _ptr(row_pos), _ptr(row_seq), kv, num_chunks, chunk_tokens,
+        _ptr(workspace), _ptr(plan), plan.numel(), n_heads, n_kv_heads, head_dim,
+        _stream(stream)))
 
 
 def rope_cache_attention_supported(kv_dtype: int, n_heads: int, n_kv_heads: int, head_dim: int,

@@ -509,11 +509,71 @@ size_t ie_hip_attention_workspace_bytes(int T, int n_heads, int head_dim, int nu
   return workspace_bytes(T, n_heads, head_dim, num_chunks);
 }
 
-int ie_hip_attention(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
-                     const int32_t* row_pos, const int32_t* row_seq, ie_kv_layout kv,
-                     int num_chunks, int chunk_tokens, void* workspace, int n_heads,
-                     int n_kv_heads, int head_dim, hipStream_t stream) {
+size_t ie_hip_attention_plan_ints(int T, int num_chunks, int chunk_tokens) {
+  if (T <= 0 || num_chunks <= 0 || chunk_tokens < IE_HIP_PAGE_SIZE || chunk_tokens > 1024 ||
+      chunk_tokens % IE_HIP_PAGE_SIZE)
+    return 0;
+  return plan_ints(T, num_chunks, chunk_tokens);
+}
+
+int ie_hip_attention_plan(int32_t* plan, size_t plan_capacity, int T, const int32_t* row_pos,
+                          const int32_t* row_seq, const int32_t* tables, int max_seqs,
+                          int max_pages, int num_chunks, int chunk_tokens) {
   clear_error();
+  if (T < 0 || num_chunks <= 0 || max_seqs <= 0 || max_pages <= 0)
+    return fail(IE_HIP_EINVAL, "attention_plan: bad row, chunk, sequence or page count");
+  if (chunk_tokens < IE_HIP_PAGE_SIZE || chunk_tokens > 1024 || chunk_tokens % IE_HIP_PAGE_SIZE)
+    return fail(IE_HIP_EINVAL, "attention_plan: chunk_tokens must be a multiple of 16 in [16, 1024]");
+  if (!plan || (T > 0 && (!row_pos || !row_seq || !tables)))
+    return fail(IE_HIP_EINVAL, "attention_plan: null pointer");
+  const size_t need = plan_ints(std::max(T, 1), num_chunks, chunk_tokens);
+  if (plan_capacity < need)
+    return fail(IE_HIP_EINVAL, "attention_plan: the plan holds " + std::to_string(plan_capacity) +
+                                   " ints; " + std::to_string(T) + " rows x " +
+                                   std::to_string(num_chunks) + " chunks need " +
+                                   std::to_string(need) + " (ie_hip_attention_plan_ints)");
+  const int stride = plan_stride(chunk_tokens), pages = chunk_tokens / IE_HIP_PAGE_SIZE;
+  int items = 0;
+  // Items in the order the kernel's own row scan numbers its workgroups: row 0's
+  // chunks, then row 1's, ...; min(p / chunk + 1, num_chunks) chunks per row.
+  for (int t = 0; t < T; ++t) {
+    const int p = row_pos[t];
+    if (p < 0) continue;
+    const int seq = row_seq[t];
+    if (seq < 0 || seq >= max_seqs)
+      return fail(IE_HIP_EINVAL, "attention_plan: row " + std::to_string(t) + " has sequence " +
+                                     std::to_string(seq) + " outside the table's " +
+                                     std::to_string(max_seqs) + " rows");
+    const int nc = std::min(p / chunk_tokens + 1, num_chunks);
+    for (int c = 0; c < nc; ++c) {
+      int32_t* it = plan + kPlanHeader + size_t(items) * stride;
+      it[0] = t;
+      it[1] = c;
+      it[2] = p;
+      it[3] = seq;
+      for (int j = 0; j < stride - 4; ++j) {
+        const int pi = c * pages + j;
+        const bool in = j < pages && pi * IE_HIP_PAGE_SIZE <= p && pi < max_pages;
+        it[4 + j] = in ? tables[size_t(seq) * max_pages + pi] : -1;
+      }
+      ++items;
+    }
+  }
+  plan[0] = items;
+  plan[1] = chunk_tokens;
+  plan[2] = num_chunks;
+  plan[3] = T;
+  return IE_HIP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int attention_call(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                   const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
+                   int num_chunks, int chunk_tokens, void* workspace, int n_heads,
+                   int n_kv_heads, int head_dim, hipStream_t stream, const int32_t* plan) {
   if (int rc = check_layout(kv, "attention")) return rc;
   if (head_dim != 64) return fail(IE_HIP_EINVAL, "attention: head_dim must be 64");
   if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads / n_kv_heads > 8)
@@ -530,7 +590,7 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
   if (impl != IE_HIP_IMPL_VALU &&
       decode_mfma_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens))
     return decode_mfma(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
-                       workspace, n_heads, n_kv_heads, stream);
+                       workspace, n_heads, n_kv_heads, stream, nullptr, plan);
   if (impl != IE_HIP_IMPL_VALU &&
       decode_mfma_f32_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens))
     return decode_mfma_f32(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks,
@@ -541,6 +601,45 @@ int ie_hip_attention(float* out, const float* q, const void* k_pool, const void*
                                "up to 1024; f32 KV: a multiple of 16 up to 1024)");
   return decode_valu(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
                      workspace, n_heads, n_kv_heads, stream);
+}
+
+int check_plan(const int32_t* plan, size_t plan_capacity, int T, int num_chunks, int chunk_tokens,
+               const char* who) {
+  if (!plan) return fail(IE_HIP_EINVAL, std::string(who) + ": null plan");
+  if (reinterpret_cast<uintptr_t>(plan) & 15)
+    return fail(IE_HIP_EINVAL, std::string(who) + ": the plan must be 16-byte aligned");
+  const size_t need = ie_hip_attention_plan_ints(T, num_chunks, chunk_tokens);
+  if (plan_capacity < need)
+    return fail(IE_HIP_EINVAL, std::string(who) + ": the plan holds " +
+                                   std::to_string(plan_capacity) + " ints, the grid needs " +
+                                   std::to_string(need));
+  return IE_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ie_hip_attention(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
+                     const int32_t* row_pos, const int32_t* row_seq, ie_kv_layout kv,
+                     int num_chunks, int chunk_tokens, void* workspace, int n_heads,
+                     int n_kv_heads, int head_dim, hipStream_t stream) {
+  clear_error();
+  return attention_call(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
+                        workspace, n_heads, n_kv_heads, head_dim, stream, nullptr);
+}
+
+int ie_hip_attention_planned(float* out, const float* q, const void* k_pool, const void* v_pool,
+                             int T, const int32_t* row_pos, const int32_t* row_seq,
+                             ie_kv_layout kv, int num_chunks, int chunk_tokens, void* workspace,
+                             const int32_t* plan, size_t plan_capacity, int n_heads,
+                             int n_kv_heads, int head_dim, hipStream_t stream) {
+  clear_error();
+  if (T > 0)
+    if (int rc = check_plan(plan, plan_capacity, T, num_chunks, chunk_tokens, "attention_planned"))
+      return rc;
+  return attention_call(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
+                        workspace, n_heads, n_kv_heads, head_dim, stream, plan);
 }
 
 }  // extern "C"
@@ -618,13 +717,13 @@ int ie_hip_rope_cache_attention_supported(int kv_dtype, int n_heads, int n_kv_he
   return fused_supported(kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens) ? 1 : 0;
 }
 
-int ie_hip_rope_cache_attention(float* out, const float* q, const float* k, const float* v,
-                                void* k_pool, void* v_pool, const float* rope_table,
-                                int table_positions, int T, const int32_t* row_pos,
-                                const int32_t* row_seq, ie_kv_layout kv, int num_chunks,
-                                int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
-                                int head_dim, hipStream_t stream) {
-  clear_error();
+static int rope_cache_attention_call(float* out, const float* q, const float* k, const float* v,
+                                     void* k_pool, void* v_pool, const float* rope_table,
+                                     int table_positions, int T, const int32_t* row_pos,
+                                     const int32_t* row_seq, const ie_kv_layout& kv,
+                                     int num_chunks, int chunk_tokens, void* workspace,
+                                     int n_heads, int n_kv_heads, int head_dim,
+                                     hipStream_t stream, const int32_t* plan) {
   if (int rc = check_layout(kv, "rope_cache_attention")) return rc;
   if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0)
     return fail(IE_HIP_EINVAL, "rope_cache_attention: bad head counts");
@@ -653,7 +752,37 @@ int ie_hip_rope_cache_attention(float* out, const float* q, const float* k, cons
   fa.table = rope_table;
   fa.table_positions = table_positions;
   return decode_mfma(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks, chunk_tokens,
-                     workspace, n_heads, n_kv_heads, stream, &fa);
+                     workspace, n_heads, n_kv_heads, stream, &fa, plan);
+}
+
+int ie_hip_rope_cache_attention(float* out, const float* q, const float* k, const float* v,
+                                void* k_pool, void* v_pool, const float* rope_table,
+                                int table_positions, int T, const int32_t* row_pos,
+                                const int32_t* row_seq, ie_kv_layout kv, int num_chunks,
+                                int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
+                                int head_dim, hipStream_t stream) {
+  clear_error();
+  return rope_cache_attention_call(out, q, k, v, k_pool, v_pool, rope_table, table_positions, T,
+                                   row_pos, row_seq, kv, num_chunks, chunk_tokens, workspace,
+                                   n_heads, n_kv_heads, head_dim, stream, nullptr);
+}
+
+int ie_hip_rope_cache_attention_planned(float* out, const float* q, const float* k,
+                                        const float* v, void* k_pool, void* v_pool,
+                                        const float* rope_table, int table_positions, int T,
+                                        const int32_t* row_pos, const int32_t* row_seq,
+                                        ie_kv_layout kv, int num_chunks, int chunk_tokens,
+                                        void* workspace, const int32_t* plan,
+                                        size_t plan_capacity, int n_heads, int n_kv_heads,
+                                        int head_dim, hipStream_t stream) {
+  clear_error();
+  if (T > 0)
+    if (int rc = check_plan(plan, plan_capacity, T, num_chunks, chunk_tokens,
+                            "rope_cache_attention_planned"))
+      return rc;
+  return rope_cache_attention_call(out, q, k, v, k_pool, v_pool, rope_table, table_positions, T,
+                                   row_pos, row_seq, kv, num_chunks, chunk_tokens, workspace,
+                                   n_heads, n_kv_heads, head_dim, stream, plan);
 }
 
 }  // extern "C"

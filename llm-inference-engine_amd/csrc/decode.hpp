@@ -1,6 +1,8 @@
 // Internal interface of the decode-attention kernels.
 #pragma once
 
+#include <hip/hip_runtime.h>
+
 #include <cstddef>
 #include <cstdint>
 
@@ -22,6 +24,17 @@ struct FusedAppend {
   const float* table = nullptr;
   int table_positions = 0;
 };
+
+// A decode work list built on the host (ie_hip_attention_plan), one item per
+// workgroup of the 16-bit kernel in its dispatch order: int32 header
+// [items, chunk_tokens, num_chunks, rows], then per item [row, chunk, position,
+// sequence, the chunk's page ids (-1 past the row's position or its table
+// row)], padded to a multiple of 4 ints so every item is 16-byte aligned.
+constexpr int kPlanHeader = 4;
+__host__ __device__ inline int plan_stride(int chunk_tokens) { return 4 + ((chunk_tokens / IE_HIP_PAGE_SIZE + 3) & ~3); }
+inline size_t plan_ints(int T, int num_chunks, int chunk_tokens) {
+  return kPlanHeader + size_t(T) * num_chunks * plan_stride(chunk_tokens);
+}
 
 struct Workspace {
   float* part_o = nullptr;     // [T][n_heads][num_chunks][head_dim] unnormalised partial outputs
@@ -51,7 +64,7 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
                 const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
                 hipStream_t stream,
-                const FusedAppend* fused = nullptr);
+                const FusedAppend* fused = nullptr, const int32_t* plan = nullptr);
 
 int decode_valu(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                 const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,

@@ -152,7 +152,8 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
                     const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
                     const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
                     const int32_t* __restrict__ tables, int T, int max_pages, int num_pages,
-                    int n_heads, int group, int num_chunks, int chunk_tokens, FusedAppend fa) {
+                    int n_heads, int group, int num_chunks, int chunk_tokens, FusedAppend fa,
+                    const int32_t* __restrict__ plan) {
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
@@ -160,31 +161,51 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = kOneWave ? 0 : __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, r = lane & 15;
+  const int waves = kOneWave ? 1 : blockDim.x >> 6;
+  const int tw = chunk_tokens / waves;              // positions per wave (a multiple of 32)
+  const int wt0 = wave * tw;                        // first position of this wave in the chunk
+
+  // Which (row, chunk) this workgroup takes, and the page ids of the wave's
+  // pages, one per lane (lane i: page i of the wave's positions; -1 past them
+  // or past the table row). With a host-built plan both come from the
+  // workgroup's item in one round trip (the header and this lane's page id are
+  // loaded together, before the item count is checked: every item slot of the
+  // grid lies inside the plan). Without one, every wave prefix-sums the rows'
+  // chunk counts (locate_chunk) and then reads the row's table: two dependent
+  // round trips before the first K/V load. A pair's ids are read from this
+  // register (readlane): a scalar load of the table inside the pair loop would
+  // share lgkmcnt with the transposed V reads, so the first V wait of every
+  // pair would also wait for the table's round trip. A wave covers at most 64
+  // pages (1,024 positions, the largest chunk).
   int t, c, p, seq;
-  if (!locate_chunk(blockIdx.x, T, row_pos, row_seq, num_chunks, chunk_tokens, lane, t, c, p, seq))
+  int pid_plan = -1;
+  if (plan) {
+    const int32_t* item = plan + kPlanHeader + size_t(blockIdx.x) * plan_stride(chunk_tokens);
+    const int pg = wt0 / IE_HIP_PAGE_SIZE + lane;
+    pid_plan = pg < chunk_tokens / IE_HIP_PAGE_SIZE ? item[4 + pg] : -1;
+    const int items = __builtin_amdgcn_readfirstlane(plan[0]);
+    t = __builtin_amdgcn_readfirstlane(item[0]);
+    c = __builtin_amdgcn_readfirstlane(item[1]);
+    p = __builtin_amdgcn_readfirstlane(item[2]);
+    seq = __builtin_amdgcn_readfirstlane(item[3]);
+    if (int(blockIdx.x) >= items) return;  // past the plan's last item
+  } else if (!locate_chunk(blockIdx.x, T, row_pos, row_seq, num_chunks, chunk_tokens, lane, t, c,
+                           p, seq)) {
     return;  // past the batch's last chunk: the whole workgroup leaves
+  }
   const int s0 = c * chunk_tokens;
   const int n = min(s0 + chunk_tokens, p + 1) - s0;  // positions of this chunk
   // The row has one chunk (its context fits one, or the caller sized one):
   // written here; the merge skips it, reading the same count.
   const bool single = min(p / chunk_tokens + 1, num_chunks) == 1;
-  const int waves = kOneWave ? 1 : blockDim.x >> 6;
-  const int tw = chunk_tokens / waves;              // positions per wave (a multiple of 32)
-  const int wt0 = wave * tw;                        // first position of this wave in the chunk
   const int nw = min(max(n - wt0, 0), tw);          // positions this wave attends to
   const int np = (nw + 31) >> 5;                    // its page pairs
   unsigned char* warea = smem + size_t(wave) * kTile;
   const unsigned warea_lds = lds_address(smem) + wave * kTile;
-
-  // Page ids of the wave's pages, one per lane (lane i: page i of the wave's
-  // positions; -1 past them or past the table row), loaded once. A pair's ids
-  // are read from this register (readlane): a scalar load of the table inside
-  // the pair loop would share lgkmcnt with the transposed V reads, so the
-  // first V wait of every pair would also wait for the table's round trip.
-  // A wave covers at most 64 pages (1,024 positions, the largest chunk).
   const int pi0 = (s0 + wt0) / IE_HIP_PAGE_SIZE;
   const int32_t* row_tab = tables + size_t(seq) * max_pages;
-  const int pid_lane = (16 * lane < nw && pi0 + lane < max_pages) ? row_tab[pi0 + lane] : -1;
+  const int pid_lane = plan ? (16 * lane < nw ? pid_plan : -1)
+                            : (16 * lane < nw && pi0 + lane < max_pages) ? row_tab[pi0 + lane] : -1;
   auto page_id = [&](const int pw) -> int {
     return pw < 64 ? __builtin_amdgcn_readlane(pid_lane, pw) : -1;
   };
@@ -732,7 +753,7 @@ static int decode_mfma_waves(int chunk_tokens, int64_t slots) {
 int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                 const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
                 int num_chunks, int chunk_tokens, void* workspace, int n_heads, int n_kv_heads,
-                hipStream_t stream, const FusedAppend* fused) {
+                hipStream_t stream, const FusedAppend* fused, const int32_t* plan) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
   const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
   const int waves = decode_mfma_waves(chunk_tokens, slots);
@@ -761,7 +782,8 @@ int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_po
     }                                                                                             \
     hipLaunchKernelGGL((decode_partial_mfma<KVT, ONE, FUSED>), grid, block, lds, stream, out,     \
                        ws.part_o, ws.part_ml, q, kp, vp, row_pos, row_seq, kv.tables, T,          \
-                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens, fa); \
+                       kv.max_pages, kv.num_pages, n_heads, group, num_chunks, chunk_tokens, fa,  \
+                       plan);                                                                     \
   } while (0)
 #define IE_DECODE_LAUNCH_KV(KVT)                 \
   if (fused) {                                   \
