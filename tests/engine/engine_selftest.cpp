@@ -150,12 +150,17 @@ struct Harness {
     std::fflush(stdout);
     op();
     const ie::hip::StepInfo& si = eng->last_step();
-    char path[160];
-    std::snprintf(path, sizeof(path), "%s: path graph=%d prompt=%d fused=%d chunk=%d x %d", name.c_str(),
-                  si.graph, si.prompt, si.fused, si.chunk_tokens, si.chunks);
+    // Flash-decoding steps of a 16-bit cache that fit one launch read the work
+    // list the engine builds on the host; prompts and f32 caches do not.
+    const bool want_planned = !si.prompt && eng->kv_dtype() != IE_KV_F32 &&
+                              T <= std::max(eng->max_batch(), 16);
+    char path[200];
+    std::snprintf(path, sizeof(path), "%s: path graph=%d prompt=%d fused=%d planned=%d chunk=%d x %d",
+                  name.c_str(), si.graph, si.prompt, si.fused, si.planned, si.chunk_tokens,
+                  si.chunks);
     result(si.rows == T && (want_graph < 0 || si.graph == bool(want_graph)) &&
                (want_prompt < 0 || si.prompt == bool(want_prompt)) &&
-               (want_fused < 0 || si.fused == bool(want_fused)),
+               (want_fused < 0 || si.fused == bool(want_fused)) && si.planned == want_planned,
            path);
 
     const size_t tab_n = size_t(eng->max_batch()) * eng->max_pages_per_seq();
