@@ -481,20 +481,17 @@ int ie_hip_attention_chunks(int context_tokens, int chunk_tokens) {
 }
 
 int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
-  const int cus = device_compute_units();
-  const int64_t rows = std::max(T, 1);
-  const int ctx = std::max(max_context, 1);
   if (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) {
     // Matrix-core kernel (measured on MI355X): 128-position chunks. Where that
     // gives two workgroups per compute unit one wave streams each chunk; on
     // smaller grids the kernel gives each of a chunk's four page pairs its own
     // wave (same result), so all are in flight at once, and the merge reads half
     // the partials 64-position chunks would make.
-    (void)rows;
-    (void)ctx;
-    (void)cus;
     return 128;
   }
+  const int cus = device_compute_units();
+  const int64_t rows = std::max(T, 1);
+  const int ctx = std::max(max_context, 1);
   // float32 (matrix-core kernel, one page in flight per wave; measured on
   // MI355X): the largest chunk up to 256 positions that still gives two
   // workgroups per compute unit -- long chains of pages per wave where the grid

@@ -23,35 +23,41 @@
 //
 // Precision (2e-3 absolute bound for 16-bit caches): K and V enter the MFMA in
 // their stored format, exactly. Q (pre-scaled by log2(e)/8) and P are split
-// into hi + lo halves of the same 16-bit type (x = hi + lo, |x - hi - lo| ~
-// 2^-22 |x|), each product done twice: float32-level scores and weights.
+// into hi + lo halves of the same 16-bit type, each product done twice:
+// |x - hi - lo| <= u^2 |x| for the type's unit roundoff u (f16 2^-11, so
+// 2^-22: float32-level; bf16 2^-8, so 2^-16).
 //
 // Layout of the work:
-//   One workgroup per non-empty (row, chunk) pair, with one wave per 128
-//   positions of the chunk (decode_mfma_waves); each wave streams its positions
-//   as page pairs (32 tokens, 2 pages), keeping the next pair's loads in flight
-//   while it computes the current one. The 1-D grid is numbered row by row over
-//   the chunks each row actually has (a prefix sum of the rows' chunk counts,
-//   computed by every wave from row_pos), so all real work comes first in
-//   dispatch order and the slots past the batch's total exit at once: no empty
-//   workgroup holds a CU while real ones wait. A wave takes 16 KB of LDS (two V
-//   page-pair tiles, double-buffered), so a CU holds 10 waves.
+//   One workgroup per non-empty (row, chunk) pair. The 1-D grid is numbered row
+//   by row over the chunks each row actually has, so all real work comes first
+//   in dispatch order and the slots past the batch's total exit at once. A
+//   workgroup finds its (row, chunk) and page ids either in a host-built work
+//   list (one load) or by a prefix sum of the rows' chunk counts from row_pos
+//   followed by the row's table (two dependent loads).
+//   A chunk is streamed as page pairs (32 tokens, 2 pages), and each pair
+//   yields its own partial: its max per head, weights relative to that max,
+//   their sum and V^T P^T from zero (fold_pair folds it into the running
+//   result). Large grids: one wave streams the chunk's pairs, keeping the next
+//   pair's loads in flight while it computes the current one. Small grids (few,
+//   long rows): one wave per pair, every pair in flight at once, and wave 0
+//   folds the others' partials through LDS in pair order -- the same fold, so
+//   the same bits (decode_mfma_waves). A wave takes 16 KB of LDS (two V
+//   page-pair tiles, double-buffered).
 //   1. The query, then page pair 0: K straight into the MFMA A-operand
 //      registers (lanes 0-15 hold tokens 0-15, the 4 lane groups the 4 16-byte
 //      slices of each 64-byte quarter row), V into an LDS tile by DMA.
 //   2. Per page pair, as its data lands: S^T (8 MFMA 16x16x32 per page); the
-//      next pair's loads into the other K registers and LDS tile; the online
-//      softmax update (running max and sum per head, base 2); O^T += V^T P^T,
-//      V^T read back from the tile transposed (ds_read_b64_tr_b16) as the A
-//      operand (16 MFMA per pair).
-//   3. Waves of one workgroup are merged through LDS. A row whose context fits
-//      one chunk writes `out` directly; otherwise the chunk writes its partial
-//      (o, m, l) to the workspace and decode_merge_kernel (decode.hip) combines
-//      the row's chunks. Fusing that merge into this kernel (the row's last
-//      chunk to finish merges, through a per-row atomic counter and
-//      device-coherent stores and loads) was measured slower on MI355X: its
-//      tail is three dependent memory round trips (store completion, the
-//      atomic, the partials) against one launch plus one round trip.
+//      next pair's loads into the K registers and the other LDS tile; the
+//      pair's max, weights and sum; V^T P^T with V^T read back from the tile
+//      transposed (ds_read_b64_tr_b16) as the A operand (16 MFMA per pair);
+//      the fold.
+//   3. A row whose context fits one chunk writes `out` directly; otherwise the
+//      chunk writes its partial (o, m, l) to the workspace and
+//      decode_merge_kernel (decode.hip) combines the row's chunks. Fusing that
+//      merge into this kernel (the row's last chunk to finish merges, through a
+//      per-row atomic counter) was measured slower on MI355X, also with every
+//      chunk of a row placed on one XCD so the partials stay in its L2: the
+//      store acknowledgements and the atomic cost what the launch saves.
 //   Positions past the row's context (the tail of its last page) and pages
 //   whose id lies outside the pool are masked: their scores are -inf and their
 //   V elements are zeroed before the product, so stale or non-finite memory in
@@ -141,9 +147,10 @@ __device__ __forceinline__ bool locate_chunk(int wg, int T, const int32_t* __res
   return false;
 }
 
-// kOneWave: one-wave workgroups (chunks of up to 255 tokens) -- the wave's
-// softmax is the chunk's, so the epilogue writes straight from the
-// accumulators and the workgroup needs no LDS beyond its V tiles.
+// kOneWave: one-wave workgroups (a wave streams the whole chunk) -- its fold
+// is the chunk's result, so the epilogue writes straight from the accumulators
+// and the workgroup needs no LDS beyond its V tiles. Otherwise one wave per
+// page pair, and wave 0 folds the other waves' pair partials through LDS.
 template <int KV, bool kOneWave, bool kFused>
 __global__ void __launch_bounds__(kOneWave ? 64 : 512)
 __attribute__((amdgpu_waves_per_eu(2)))  // ~206 registers: a pair partial beside the running one
@@ -366,9 +373,10 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     }
   }
 
-  // Per page pair j, as its data lands: scores, online softmax, O^T += V^T P^T,
-  // with the loads of pair j+1 issued as soon as pair j's K registers are
-  // consumed, so a wave always has one pair in flight while it computes.
+  // Per page pair j, as its data lands: scores, the pair's partial (max,
+  // weights, sum, V^T P^T) and its fold, with the loads of pair j+1 issued as
+  // soon as pair j's K registers are consumed, so a wave always has one pair in
+  // flight while it computes.
   // Lane (g, r): head r; S^T element i of the pair's page h is token
   // 32 j + 16 h + 4g + i of the wave.
   float m = -INFINITY, l = 0.0f;  // running max (base 2) and this lane's part of the sum
