@@ -171,7 +171,9 @@ int ie_hip_attention_noalloc(float* out, const float* q, const void* k_pool, con
  * ie_hip_attention_plan: writes the plan to HOST memory `plan` (capacity
  * plan_capacity ints) from host row_pos / row_seq [T] and the host table
  * [max_seqs * max_pages]; pages past a row's position or its table row are
- * -1, and ids outside the pool are left for the kernel to skip. Copy it to the
+ * -1, and ids outside the pool are left for the kernel to skip. Items are
+ * ordered longer chunks first (the rows' full chunks, then their shorter last
+ * ones), which shortens the launch's tail; the order changes no result. Copy it to the
  * device (16-byte aligned) before the launch that uses it; it must describe
  * that launch's rows, positions, chunk_tokens and num_chunks.
  * ie_hip_attention_planned / ie_hip_rope_cache_attention_planned: as

@@ -22,6 +22,7 @@
 //   M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L.
 #include <algorithm>
 #include <mutex>
+#include <vector>
 
 #include "common.hpp"
 #include "decode.hpp"
@@ -530,9 +531,15 @@ int ie_hip_attention_plan(int32_t* plan, size_t plan_capacity, int T, const int3
                                    std::to_string(num_chunks) + " chunks need " +
                                    std::to_string(need) + " (ie_hip_attention_plan_ints)");
   const int stride = plan_stride(chunk_tokens), pages = chunk_tokens / IE_HIP_PAGE_SIZE;
-  int items = 0;
-  // Items in the order the kernel's own row scan numbers its workgroups: row 0's
-  // chunks, then row 1's, ...; min(p / chunk + 1, num_chunks) chunks per row.
+  // min(p / chunk + 1, num_chunks) chunks per row. Items in dispatch order:
+  // longer chunks first -- every row's full chunks, then the shorter last
+  // chunks, longest first -- each group in row and chunk order, so the short
+  // workgroups fill the end of the launch instead of holding its start (the
+  // order changes no result: every item writes its own (row, chunk) slot).
+  struct Item {
+    int n, t, c;  // positions in the chunk, row, chunk
+  };
+  std::vector<Item> order;
   for (int t = 0; t < T; ++t) {
     const int p = row_pos[t];
     if (p < 0) continue;
@@ -542,19 +549,26 @@ int ie_hip_attention_plan(int32_t* plan, size_t plan_capacity, int T, const int3
                                      std::to_string(seq) + " outside the table's " +
                                      std::to_string(max_seqs) + " rows");
     const int nc = std::min(p / chunk_tokens + 1, num_chunks);
-    for (int c = 0; c < nc; ++c) {
-      int32_t* it = plan + kPlanHeader + size_t(items) * stride;
-      it[0] = t;
-      it[1] = c;
-      it[2] = p;
-      it[3] = seq;
-      for (int j = 0; j < stride - 4; ++j) {
-        const int pi = c * pages + j;
-        const bool in = j < pages && pi * IE_HIP_PAGE_SIZE <= p && pi < max_pages;
-        it[4 + j] = in ? tables[size_t(seq) * max_pages + pi] : -1;
-      }
-      ++items;
+    for (int c = 0; c < nc; ++c)
+      order.push_back(Item{std::min(chunk_tokens, p + 1 - c * chunk_tokens), t, c});
+  }
+  std::stable_sort(order.begin(), order.end(),
+                   [](const Item& a, const Item& b) { return a.n > b.n; });
+  int items = 0;
+  for (const Item& e : order) {
+    const int t = e.t, c = e.c;
+    const int p = row_pos[t], seq = row_seq[t];
+    int32_t* it = plan + kPlanHeader + size_t(items) * stride;
+    it[0] = t;
+    it[1] = c;
+    it[2] = p;
+    it[3] = seq;
+    for (int j = 0; j < stride - 4; ++j) {
+      const int pi = c * pages + j;
+      const bool in = j < pages && pi * IE_HIP_PAGE_SIZE <= p && pi < max_pages;
+      it[4 + j] = in ? tables[size_t(seq) * max_pages + pi] : -1;
     }
+    ++items;
   }
   plan[0] = items;
   plan[1] = chunk_tokens;

@@ -28,12 +28,13 @@
 // 2^-22: float32-level; bf16 2^-8, so 2^-16).
 //
 // Layout of the work:
-//   One workgroup per non-empty (row, chunk) pair. The 1-D grid is numbered row
-//   by row over the chunks each row actually has, so all real work comes first
-//   in dispatch order and the slots past the batch's total exit at once. A
-//   workgroup finds its (row, chunk) and page ids either in a host-built work
-//   list (one load) or by a prefix sum of the rows' chunk counts from row_pos
-//   followed by the row's table (two dependent loads).
+//   One workgroup per non-empty (row, chunk) pair. The 1-D grid covers the
+//   chunks each row actually has, so all real work comes first in dispatch
+//   order and the slots past the batch's total exit at once. A workgroup finds
+//   its (row, chunk) and page ids either in a host-built work list (one load;
+//   items ordered longer chunks first, so the rows' short last chunks fill the
+//   end of the launch) or by a prefix sum of the rows' chunk counts from
+//   row_pos followed by the row's table (two dependent loads; row by row).
 //   A chunk is streamed as page pairs (32 tokens, 2 pages), and each pair
 //   yields its own partial: its max per head, weights relative to that max,
 //   their sum and V^T P^T from zero (fold_pair folds it into the running

@@ -2,8 +2,9 @@
 
 The planner is host code in libie_hip.so: it runs without a GPU. Its output is
 checked against a plain restatement of the layout include/ie_hip.h documents --
-header [items, chunk_tokens, num_chunks, rows]; one item per (row, chunk) in row
-order, min(p / chunk + 1, num_chunks) chunks per row, none for p < 0; an item is
+header [items, chunk_tokens, num_chunks, rows]; one item per (row, chunk),
+min(p / chunk + 1, num_chunks) chunks per row, none for p < 0, longer chunks first
+(row and chunk order among chunks of one length); an item is
 [row, chunk, position, sequence, the chunk's page ids], ids -1 for pages past the
 row's position or its table row, padded to a multiple of 4 ints -- and on its
 errors. Whether the kernels read it right is tests/test_gpu_plan.py's part (bit
@@ -30,7 +31,9 @@ def restated_plan(row_pos, row_seq, tables, num_chunks, chunk_tokens):
                 pi = c * pages + j
                 ok = j < pages and pi * PAGE <= p and pi < max_pages
                 it.append(int(tables[s, pi]) if ok else -1)
-            items.append(it)
+            items.append((min(chunk_tokens, p + 1 - c * chunk_tokens), it))
+    # dispatch order: longer chunks first, row and chunk order within a length (stable)
+    items = [it for _, it in sorted(items, key=lambda e: -e[0])]
     return [len(items), chunk_tokens, num_chunks, len(row_pos)], items, stride
 
 
