@@ -241,72 +241,36 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   // fmaf, no contraction; the KV type's own rounding), so pages and results
   // are bit-identical to the two calls. Rows whose position lies outside the
   // table are not appended and use their query unrotated, as there.
+  // The cos/sin row and the new k and v are loaded here and used only after
+  // pair 0's K/V loads are issued, so their round trip overlaps that one; the
+  // slot's page id is the wave's own (page_id), not another table read.
   const bool app = kFused && p < fa.table_positions;
   const int off = p - s0 - wt0;  // position p within this wave's range
   const bool own = app && off >= 0 && off < tw;
   E kn[4][8];                    // new K row, this lane's slices (dims 8g + 32 ks + e)
   uint4 vn = make_uint4(0, 0, 0, 0);  // new V row, 16-byte piece r
+  float4 tc0, tc1, tn0, tn1;          // cos and sin of position p, dims 8g .. 8g+7
+  float4 kr[2][4];                    // new k, KV head hk: dims 64 hk + 8g .. +7, 32 + ..
+  float4 vr0, vr1;                    // new v, dims 8r .. 8r+7
   if constexpr (kFused) {
     if (app) {
       const float* trow = fa.table + size_t(p) * 64 + 8 * g;
-      const float4 c0 = *reinterpret_cast<const float4*>(trow);
-      const float4 c1 = *reinterpret_cast<const float4*>(trow + 4);
-      const float4 n0 = *reinterpret_cast<const float4*>(trow + 32);
-      const float4 n1 = *reinterpret_cast<const float4*>(trow + 36);
-      const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-      const float sn[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
-      auto rotate = [&](float4& a0, float4& a1, float4& b0, float4& b1) {
-        float x0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        float x1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-        float r0[8], r1[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          r0[e] = __builtin_fmaf(x0[e], cs[e], -(x1[e] * sn[e]));  // x0*c - x1*s
-          r1[e] = __builtin_fmaf(x1[e], cs[e], x0[e] * sn[e]);     // x1*c + x0*s
-        }
-        a0 = make_float4(r0[0], r0[1], r0[2], r0[3]);
-        a1 = make_float4(r0[4], r0[5], r0[6], r0[7]);
-        b0 = make_float4(r1[0], r1[1], r1[2], r1[3]);
-        b1 = make_float4(r1[4], r1[5], r1[6], r1[7]);
-      };
-      rotate(q0a, q0b, q1a, q1b);
+      tc0 = *reinterpret_cast<const float4*>(trow);
+      tc1 = *reinterpret_cast<const float4*>(trow + 4);
+      tn0 = *reinterpret_cast<const float4*>(trow + 32);
+      tn1 = *reinterpret_cast<const float4*>(trow + 36);
       if (own) {
         const float4* krow = reinterpret_cast<const float4*>(fa.k + size_t(t) * kKvd + 8 * g);
 #pragma unroll
-        for (int hk = 0; hk < 2; ++hk) {  // KV head hk: dims 64 hk + (8g .. 8g+7, 32 + ..)
-          float4 a0 = krow[16 * hk], a1 = krow[16 * hk + 1];
-          float4 b0 = krow[16 * hk + 8], b1 = krow[16 * hk + 9];
-          rotate(a0, a1, b0, b1);
-          const float ra[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-          const float rb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            kn[2 * hk][e] = __builtin_bit_cast(E, static_cast<uint16_t>(Kv<KV>::narrow(ra[e])));
-            kn[2 * hk + 1][e] = __builtin_bit_cast(E, static_cast<uint16_t>(Kv<KV>::narrow(rb[e])));
-          }
+        for (int hk = 0; hk < 2; ++hk) {
+          kr[hk][0] = krow[16 * hk];
+          kr[hk][1] = krow[16 * hk + 1];
+          kr[hk][2] = krow[16 * hk + 8];
+          kr[hk][3] = krow[16 * hk + 9];
         }
         const float4* vrow = reinterpret_cast<const float4*>(fa.v + size_t(t) * kKvd + 8 * r);
-        const float4 v0 = vrow[0], v1 = vrow[1];
-        vn.x = Kv<KV>::narrow(v0.x) | (Kv<KV>::narrow(v0.y) << 16);
-        vn.y = Kv<KV>::narrow(v0.z) | (Kv<KV>::narrow(v0.w) << 16);
-        vn.z = Kv<KV>::narrow(v1.x) | (Kv<KV>::narrow(v1.y) << 16);
-        vn.w = Kv<KV>::narrow(v1.z) | (Kv<KV>::narrow(v1.w) << 16);
-        // The append itself: K slices from lanes (g, p % 16), V pieces from lanes
-        // (0, r); skipped, like ie_hip_rope_and_cache, when the page is outside
-        // the pool.
-        const int pidx = p / IE_HIP_PAGE_SIZE;
-        const int pid = pidx < max_pages ? tables[size_t(seq) * max_pages + pidx] : -1;
-        if (pid >= 0 && pid < num_pages) {
-          const size_t row = (size_t(pid) * IE_HIP_PAGE_SIZE + (p & 15)) * kKvd;
-          if (r == (p & 15)) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-              *reinterpret_cast<op*>(fa.k_pool + row + 8 * g + 32 * ks) =
-                  op{kn[ks][0], kn[ks][1], kn[ks][2], kn[ks][3],
-                     kn[ks][4], kn[ks][5], kn[ks][6], kn[ks][7]};
-          }
-          if (g == 0) *reinterpret_cast<uint4*>(fa.v_pool + row + 8 * r) = vn;
-        }
+        vr0 = vrow[0];
+        vr1 = vrow[1];
       }
     }
   }
@@ -346,6 +310,63 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
   int cur_a = page_id(0), cur_b = page_id(1);
   int nx_a = page_id(2), nx_b = page_id(3);
   if (np > 0) issue(0, valid(cur_a) ? cur_a : 0, valid(cur_b) ? cur_b : 0);
+
+  if constexpr (kFused) {
+    if (app) {
+      const float cs[8] = {tc0.x, tc0.y, tc0.z, tc0.w, tc1.x, tc1.y, tc1.z, tc1.w};
+      const float sn[8] = {tn0.x, tn0.y, tn0.z, tn0.w, tn1.x, tn1.y, tn1.z, tn1.w};
+      auto rotate = [&](float4& a0, float4& a1, float4& b0, float4& b1) {
+        float x0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        float x1[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float r0[8], r1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          r0[e] = __builtin_fmaf(x0[e], cs[e], -(x1[e] * sn[e]));  // x0*c - x1*s
+          r1[e] = __builtin_fmaf(x1[e], cs[e], x0[e] * sn[e]);     // x1*c + x0*s
+        }
+        a0 = make_float4(r0[0], r0[1], r0[2], r0[3]);
+        a1 = make_float4(r0[4], r0[5], r0[6], r0[7]);
+        b0 = make_float4(r1[0], r1[1], r1[2], r1[3]);
+        b1 = make_float4(r1[4], r1[5], r1[6], r1[7]);
+      };
+      rotate(q0a, q0b, q1a, q1b);
+      if (own) {
+#pragma unroll
+        for (int hk = 0; hk < 2; ++hk) {  // KV head hk: dims 64 hk + (8g .. 8g+7, 32 + ..)
+          rotate(kr[hk][0], kr[hk][1], kr[hk][2], kr[hk][3]);
+          const float ra[8] = {kr[hk][0].x, kr[hk][0].y, kr[hk][0].z, kr[hk][0].w,
+                               kr[hk][1].x, kr[hk][1].y, kr[hk][1].z, kr[hk][1].w};
+          const float rb[8] = {kr[hk][2].x, kr[hk][2].y, kr[hk][2].z, kr[hk][2].w,
+                               kr[hk][3].x, kr[hk][3].y, kr[hk][3].z, kr[hk][3].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            kn[2 * hk][e] = __builtin_bit_cast(E, static_cast<uint16_t>(Kv<KV>::narrow(ra[e])));
+            kn[2 * hk + 1][e] = __builtin_bit_cast(E, static_cast<uint16_t>(Kv<KV>::narrow(rb[e])));
+          }
+        }
+        vn.x = Kv<KV>::narrow(vr0.x) | (Kv<KV>::narrow(vr0.y) << 16);
+        vn.y = Kv<KV>::narrow(vr0.z) | (Kv<KV>::narrow(vr0.w) << 16);
+        vn.z = Kv<KV>::narrow(vr1.x) | (Kv<KV>::narrow(vr1.y) << 16);
+        vn.w = Kv<KV>::narrow(vr1.z) | (Kv<KV>::narrow(vr1.w) << 16);
+        // The append itself: K slices from lanes (g, p % 16), V pieces from lanes
+        // (0, r); skipped, like ie_hip_rope_and_cache, when the page is outside
+        // the table row or the pool. The loads of pair 0 above read the slot's
+        // old contents; the loop substitutes the new row for them.
+        const int pid = page_id(off >> 4);
+        if (pid >= 0 && pid < num_pages) {
+          const size_t row = (size_t(pid) * IE_HIP_PAGE_SIZE + (p & 15)) * kKvd;
+          if (r == (p & 15)) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+              *reinterpret_cast<op*>(fa.k_pool + row + 8 * g + 32 * ks) =
+                  op{kn[ks][0], kn[ks][1], kn[ks][2], kn[ks][3],
+                     kn[ks][4], kn[ks][5], kn[ks][6], kn[ks][7]};
+          }
+          if (g == 0) *reinterpret_cast<uint4*>(fa.v_pool + row + 8 * r) = vn;
+        }
+      }
+    }
+  }
 
   // Query times log2(e)/8, split into hi + lo, as the B operands of the 4
   // 32-dim steps of the 128-dim KV row: head r's values in the two steps of its
