@@ -18,14 +18,16 @@
 //      value row read once for all heads of the group; butterfly-reduced over
 //      the 8 positions, then across waves through LDS.
 //   A row whose context fits one chunk writes `out` directly; otherwise the
-//   chunk writes (o, m, l) and decode_merge_kernel combines them:
-//   M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L.
+//   chunk writes (o, m, l), m in log2 units (every partial kernel: the VALU one
+//   here converts its natural-log max), and decode_merge_kernel combines them:
+//   M = max m_c, L = sum l_c 2^(m_c - M), out = sum o_c 2^(m_c - M) / L.
 #include <algorithm>
 #include <mutex>
 #include <vector>
 
 #include "common.hpp"
 #include "decode.hpp"
+#include "mfma.hpp"
 
 namespace iehip {
 namespace {
@@ -33,6 +35,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxChunk = 1024;
+constexpr float kLog2eMerge = 1.4426950408889634f;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -215,12 +218,13 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
   }
   if (chunks_row > 1 && tid < G) {
     const size_t slot = (size_t(t) * n_heads + h0 + tid) * num_chunks + c;
-    part_ml[2 * slot] = stat[0][tid];
+    part_ml[2 * slot] = stat[0][tid] * kLog2eMerge;  // log2 units, as the merge takes them
     part_ml[2 * slot + 1] = stat[1][tid];
   }
 }
 
-// Split-K merge: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M), M = max m_c.
+// Split-K merge: out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M), M = max m_c
+// (m in log2 units).
 //
 // The order of the sums is fixed by the row alone, so a row's result does not
 // depend on the batch, the launch shape or the chunk count the caller sizes
@@ -233,10 +237,12 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
 //
 // A workgroup takes one (head, row) and a slice of 64/S output dims (S = 1, 2
 // or 4 slices, more slices when rows x heads alone would leave compute units
-// idle). In a wave, lane = (block lane, dim quad): the slice's Q quads of
-// float4 side by side and 64/Q block lanes; block lane i of wave w owns block
-// w * (64/Q) + i and loads its 8 chunks at once. The tree runs over lanes by
-// xor-shuffles, then over waves through LDS.
+// idle). In a wave, lane = (dim quad, block lane): the slice's Q quads of
+// float4, each over CL = 64/Q consecutive lanes; block lane i of wave w owns
+// block w * CL + i and loads its 8 chunks at once. The tree runs over the
+// block lanes -- node (b, b + k) forms in b's lane from lane b + k, a VALU
+// lane move (DPP within a row of 16 lanes, the permlane swaps across rows) --
+// and then over the waves through LDS.
 constexpr int kMergeBlock = 8;
 constexpr int kMergeMaxWaves = 16;
 
@@ -245,14 +251,14 @@ struct MergeAcc {
   float4 a;
 };
 
-// (M1, L1, A1) + (M2, L2, A2) = (M, L1 e^(M1-M) + L2 e^(M2-M), A1 e^(M1-M) +
-// A2 e^(M2-M)), M = max(M1, M2); an identity side (M = -inf) returns the
+// (M1, L1, A1) + (M2, L2, A2) = (M, L1 2^(M1-M) + L2 2^(M2-M), A1 2^(M1-M) +
+// A2 2^(M2-M)), M = max(M1, M2); an identity side (M = -inf) returns the
 // other side bit for bit.
 __device__ __forceinline__ MergeAcc merge_pair(const MergeAcc& x, const MergeAcc& y) {
   if (y.m == -INFINITY) return x;
   if (x.m == -INFINITY) return y;
   const float m = fmaxf(x.m, y.m);
-  const float ex = expf(x.m - m), ey = expf(y.m - m);
+  const float ex = __builtin_amdgcn_exp2f(x.m - m), ey = __builtin_amdgcn_exp2f(y.m - m);
   MergeAcc r;
   r.m = m;
   r.l = __builtin_fmaf(x.l, ex, y.l * ey);
@@ -263,15 +269,47 @@ __device__ __forceinline__ MergeAcc merge_pair(const MergeAcc& x, const MergeAcc
   return r;
 }
 
-__device__ __forceinline__ MergeAcc shfl_xor_acc(const MergeAcc& x, int off) {
+// The value of lane + K, for the lanes where that lane is in the same group of
+// 2K (the lanes whose bit K is clear); other lanes get an unspecified value.
+// K < 16: a DPP move within the row of 16 lanes (quad_perm for 1 and 2,
+// row_shl for 4 and 8); K = 16, 32: v_permlane16/32_swap.
+template <int K>
+__device__ __forceinline__ float lane_from_above(float x) {
+  if constexpr (K == 16 || K == 32) {
+    float a, b;  // a: the lower lane's value, b: the upper lane's, in both lanes
+    if constexpr (K == 16)
+      lane_pair16(x, a, b);
+    else
+      lane_pair32(x, a, b);
+    return b;
+  } else {
+    constexpr int ctrl = K == 1   ? 0xB1    // quad_perm [1, 0, 3, 2]
+                         : K == 2 ? 0x4E    // quad_perm [2, 3, 0, 1]
+                                  : 0x100 + K;  // row_shl:K
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                         0, __builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false));
+  }
+}
+
+template <int K>
+__device__ __forceinline__ MergeAcc acc_from_above(const MergeAcc& x) {
   MergeAcc r;
-  r.m = __shfl_xor(x.m, off, 64);
-  r.l = __shfl_xor(x.l, off, 64);
-  r.a.x = __shfl_xor(x.a.x, off, 64);
-  r.a.y = __shfl_xor(x.a.y, off, 64);
-  r.a.z = __shfl_xor(x.a.z, off, 64);
-  r.a.w = __shfl_xor(x.a.w, off, 64);
+  r.m = lane_from_above<K>(x.m);
+  r.l = lane_from_above<K>(x.l);
+  r.a.x = lane_from_above<K>(x.a.x);
+  r.a.y = lane_from_above<K>(x.a.y);
+  r.a.z = lane_from_above<K>(x.a.z);
+  r.a.w = lane_from_above<K>(x.a.w);
   return r;
+}
+
+// Levels K, 2K, ... below CL of the tree over a wave's block lanes.
+template <int K, int CL>
+__device__ __forceinline__ void lane_tree(MergeAcc& acc) {
+  if constexpr (K < CL) {
+    acc = merge_pair(acc, acc_from_above<K>(acc));
+    lane_tree<2 * K, CL>(acc);
+  }
 }
 
 // Q = dim quads per slice (16, 8 or 4 for S = 1, 2, 4); blockIdx = (head, row, slice).
@@ -284,7 +322,7 @@ decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
   __shared__ MergeAcc red[kMergeMaxWaves][Q];
   const int h = blockIdx.x, t = blockIdx.y, s = blockIdx.z;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
-  const int qd = lane % Q, bl = lane / Q;
+  const int qd = lane / CL, bl = lane % CL;
   const int p = row_pos[t];
   if (p < 0) return;
   const int nc = min(p / chunk_tokens + 1, num_chunks);
@@ -313,7 +351,7 @@ decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
     acc.m = mb;
 #pragma unroll
     for (int j = 0; j < kMergeBlock; ++j) {
-      const float e = mlc[j].x == -INFINITY ? 0.0f : expf(mlc[j].x - mb);
+      const float e = mlc[j].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mlc[j].x - mb);
       acc.l = __builtin_fmaf(mlc[j].y, e, acc.l);
       acc.a.x = __builtin_fmaf(oc[j].x, e, acc.a.x);
       acc.a.y = __builtin_fmaf(oc[j].y, e, acc.a.y);
@@ -321,13 +359,8 @@ decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
       acc.a.w = __builtin_fmaf(oc[j].w, e, acc.a.w);
     }
   }
-  // Tree over the wave's blocks: at level `off`, the lane whose block index
-  // has that bit clear is the left child. Both children end up with the node.
-#pragma unroll
-  for (int off = Q; off < 64; off <<= 1) {
-    const MergeAcc other = shfl_xor_acc(acc, off);
-    acc = (bl & (off / Q)) ? merge_pair(other, acc) : merge_pair(acc, other);
-  }
+  // Tree over the wave's blocks: the lanes with bl = 0 end up with the wave's node.
+  lane_tree<1, CL>(acc);
   float4* dst = reinterpret_cast<float4*>(out + (size_t(t) * n_heads + h) * HD + dim);
   if (W > 1) {  // the tree continues over the waves, node (w, w + stride)
     if (bl == 0) red[w][qd] = acc;

@@ -38,7 +38,7 @@ inline size_t plan_ints(int T, int num_chunks, int chunk_tokens) {
 
 struct Workspace {
   float* part_o = nullptr;     // [T][n_heads][num_chunks][head_dim] unnormalised partial outputs
-  float* part_ml = nullptr;    // [T][n_heads][num_chunks][2] partial max and sum of exp
+  float* part_ml = nullptr;    // [T][n_heads][num_chunks][2] partial max (log2 units) and sum
 };
 
 Workspace carve_workspace(void* base, int T, int n_heads, int head_dim, int num_chunks);

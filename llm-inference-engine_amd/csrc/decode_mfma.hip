@@ -80,7 +80,6 @@ constexpr int kTile = 2 * kPair;   // per-wave LDS: the two page-pair tiles; aft
 constexpr int kMaxWaves = 8;
 constexpr int kOutTile = 16 * 64 * 4;        // a wave's output tile [16 heads][64] f32
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxLds = kMaxWaves * kTile;
 
 __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
@@ -554,7 +553,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
 
   // The chunk's result per (head h, dims 4 d4 .. 4 d4 + 3): a row that fits one
   // chunk writes `out`; otherwise the chunk's partial (o unnormalised, m in
-  // natural-log units, l) goes to the workspace for decode_merge_kernel.
+  // log2 units, l) goes to the workspace for decode_merge_kernel.
   auto emit = [&](const int h, const int d4, const f32x4 acc, const float mh, const float lh) {
     const size_t head = size_t(t) * n_heads + h;
     if (single) {
@@ -562,7 +561,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     } else {
       const size_t slot = head * num_chunks + c;
       *reinterpret_cast<f32x4*>(part_o + slot * 64 + 4 * d4) = acc;
-      if (d4 == 0) *reinterpret_cast<float2*>(part_ml + 2 * slot) = make_float2(mh * kLn2, lh);
+      if (d4 == 0) *reinterpret_cast<float2*>(part_ml + 2 * slot) = make_float2(mh, lh);
     }
   };
   if (head_ok) {
@@ -753,7 +752,7 @@ decode_partial_mfma_f32(float* __restrict__ out, float* __restrict__ part_o,
   }
   if (!single && g == 0) {
     const size_t slot = head * num_chunks + c;
-    *reinterpret_cast<float2*>(part_ml + 2 * slot) = make_float2(m * kLn2, l);
+    *reinterpret_cast<float2*>(part_ml + 2 * slot) = make_float2(m, l);
   }
 }
 
