@@ -430,6 +430,10 @@ int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T,
   const int64_t pairs = int64_t(T) * n_heads;
   const int cus = device_compute_units();
   int slices = pairs >= cus ? 1 : (2 * pairs >= cus ? 2 : 4);
+  // Few rows: as many slices as make every workgroup one wave (up to 16), so
+  // that the tree ends in registers, without the LDS stage and its barriers.
+  if (pairs < cus)
+    while (slices < 16 && 4 * slices * kMergeBlock < num_chunks) slices *= 2;
   while (slices < 16 && int64_t(kMergeMaxWaves) * 4 * slices * kMergeBlock < num_chunks)
     slices *= 2;
   const int blocks_per_wave = 4 * slices;
