@@ -185,9 +185,10 @@ def test_config3_full_size(ie, O, dev, kv, impl, partition):
 @pytest.mark.parametrize("rows", [1, 12, 24])
 @pytest.mark.parametrize("kv", list(KVS))
 def test_merge_layouts(ie, O, dev, rows, kv, impl):
-    """Every split-K merge layout: rows x heads below, near and above the compute-unit
-    count (4, 2 and 1 dim slices per (head, row)) with 64-token chunks over contexts up to
-    8,192 (128 chunks: one merge wave up to four), mixed with rows that fit one chunk."""
+    """Split-K merge layouts: rows x heads below and above the compute-unit count (4 dim
+    slices of one wave per (head, row) for 1 and 12 rows; 1 slice of four waves, with the
+    LDS stage, for 24) with 64-token chunks over contexts up to 8,192 (128 chunks), mixed
+    with rows that fit one chunk."""
     rng = np.random.default_rng(100 + rows)
     lens = [8192] + [int(x) for x in rng.integers(1, 8193, rows - 1)]
     if rows > 2:
@@ -206,7 +207,8 @@ def test_merge_layouts(ie, O, dev, rows, kv, impl):
 
 def test_config4_full_size(ie, O, dev):
     """BASELINE config 4's attention: batch 1, context 32,768, bf16 KV, shuffled 16-token
-    pages, with the library's own chunk choice (512 chunks of 64 tokens)."""
+    pages, with the library's own chunk choice (256 chunks of 128 tokens: a merge of 8 dim
+    slices, its lane tree on DPP moves and v_permlane16_swap)."""
     rng = np.random.default_rng(20263)
     kvt = KVS["bf16"]
     L = 32768
@@ -219,6 +221,25 @@ def test_config4_full_size(ie, O, dev):
                              threads=8)
     got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, ct)
     check(O, got, want, kvt, f"config 4, chunk {ct}")
+
+
+@pytest.mark.parametrize("rows,L", [(1, 32768), (2, 65536)])
+def test_merge_lane_tree_widths(ie, O, dev, rows, L):
+    """The widest merge lane trees: 64-token chunks over 32,768 positions (512 chunks: 16
+    dim slices of one wave, the lane tree's last level on v_permlane32_swap) and over
+    65,536 (1,024 chunks: 16 slices of two waves, then the LDS stage)."""
+    rng = np.random.default_rng(300 + rows)
+    kvt = KVS["f16"]
+    lens = [L] + [int(x) for x in rng.integers(1, L + 1, rows - 1)]
+    tables, max_pages, num_pages = make_tables(lens, rng)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_pos = np.array([n - 1 for n in lens], np.int32)
+    row_seq = np.arange(rows, dtype=np.int32)
+    q = normal(rng, (rows, QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
+                             threads=8)
+    got = gpu_attention(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, 64)
+    check(O, got, want, kvt, f"rows {rows}, L {L}")
 
 
 @pytest.mark.parametrize("kv", ["f16", "bf16"])
