@@ -455,8 +455,8 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     // result by fold_pair. Each pair's partial depends on the pair alone, so a
     // chunk's result is the same whether one wave folds its pairs as they come
     // or several waves take one pair each and one of them folds the others'.
-    float mx = fmaxf(fmaxf(fmaxf(sa[0], sa[1]), fmaxf(sa[2], sa[3])),
-                     fmaxf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3])));
+    float mx = max_nn(max3_nn(sa[0], sa[1], sa[2]),
+                      max3_nn(max3_nn(sa[3], sb[0], sb[1]), sb[2], sb[3]));
     mx = group_max4(mx);
     const float mref = mx == -INFINITY ? 0.0f : mx;  // nothing visible: weights 0
     op phi, plo;

@@ -85,11 +85,26 @@ __device__ __forceinline__ void lane_pair16(float x, float& a, float& b) {
   b = x;
   asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
+// Maxima of values that are never NaN (scores from the matrix cores, or -inf
+// where masked): v_max_f32 / v_max3_f32 as written. fmaxf first quiets a
+// possible signalling NaN in each operand (a v_max_f32 x, x, x apiece), which
+// in the softmax loops costs as many instructions as the maxima themselves.
+// For non-NaN operands both give the same value.
+__device__ __forceinline__ float max_nn(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float max3_nn(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 __device__ __forceinline__ float group_max4(float x) {
   float a, b;
   lane_pair32(x, a, b);
-  lane_pair16(fmaxf(a, b), a, b);
-  return fmaxf(a, b);
+  lane_pair16(max_nn(a, b), a, b);
+  return max_nn(a, b);
 }
 __device__ __forceinline__ float group_sum4(float x) {
   float a, b;

@@ -343,14 +343,15 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
           op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
 #pragma unroll
           for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kt4 = 0; kt4 < 4; ++kt4)
-              mx = fmaxf(mx, fmaxf(fmaxf(s[hh][kt4][0], s[hh][kt4][1]),
-                                   fmaxf(s[hh][kt4][2], s[hh][kt4][3])));
+            const f32x4(&sh)[4] = s[hh];
+            float mx = max_nn(max3_nn(max3_nn(sh[0][0], sh[0][1], sh[0][2]),
+                                      max3_nn(sh[0][3], sh[1][0], sh[1][1]),
+                                      max3_nn(sh[1][2], sh[1][3], sh[2][0])),
+                              max3_nn(max3_nn(sh[2][1], sh[2][2], sh[2][3]),
+                                      max3_nn(sh[3][0], sh[3][1], sh[3][2]), sh[3][3]));
             mx = group_max4(mx);  // the tile's row max, relative to mref
             // m = -inf (nothing visible yet) always counts as growth when mx is finite.
-            const bool grow = m[hh] == -INFINITY ? mx != -INFINITY : mx > kLazyMax;
+            const bool grow = mx > (m[hh] == -INFINITY ? -INFINITY : kLazyMax);
             if (__builtin_amdgcn_ballot_w64(grow) != 0) {
               const float m_new = fmaxf(m[hh], mref[hh] + mx);
               // m = -inf (nothing seen yet): the old terms are all zero
