@@ -290,7 +290,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     for (int h = 0; h < 2; ++h) {
       const uint16_t* krow = k_pool + (size_t(h ? pb : pa) * IE_HIP_PAGE_SIZE + r) * kKvd + 8 * g;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) ka[h][ks] = *reinterpret_cast<const op*>(krow + 32 * ks);
+      for (int ks = 0; ks < 4; ++ks) ka[h][ks] = load_nt16<op>(krow + 32 * ks);
     }
     __builtin_amdgcn_sched_barrier(0);
     const unsigned tile = warea_lds + (j & 1) * kPair;
@@ -300,7 +300,7 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
       const int piece = r ^ (2 * (tok & 7));
       const uint16_t* src = v_pool +
           (size_t((u >> 2) ? pb : pa) * IE_HIP_PAGE_SIZE + (tok & 15)) * kKvd + 8 * piece;
-      dma16(src, tile + u * 1024);
+      dma16_nt(src, tile + u * 1024);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -648,12 +648,12 @@ decode_partial_mfma_f32(float* __restrict__ out, float* __restrict__ part_o,
     const float4* krow =
         reinterpret_cast<const float4*>(k_pool + (size_t(pid) * IE_HIP_PAGE_SIZE + r) * kKvd + 32 * g);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kv[i] = krow[i];
+    for (int i = 0; i < 8; ++i) kv[i] = krow[i];  // 8 loads per 128-byte span: cached
     __builtin_amdgcn_sched_barrier(0);
     const char* vsrc = reinterpret_cast<const char*>(v_pool) + size_t(pid) * kPageF32 + 16 * lane;
     const unsigned dst = vbuf_lds + (j & 1) * kPageF32;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) dma16(vsrc + u * 1024, dst + u * 1024);
+    for (int u = 0; u < 8; ++u) dma16_nt(vsrc + u * 1024, dst + u * 1024);
     __builtin_amdgcn_sched_barrier(0);
   };
   int cur = page_id(0), nxt = page_id(1);

@@ -67,6 +67,24 @@ __device__ __forceinline__ void dma16(const void* src, unsigned lds) {
                : "memory", "m0");
 }
 
+// Loads of data read once per launch (the decode kernels' K/V pages), with the
+// non-temporal hint. A page walk of config 3's pattern (72 MB of 4 KB pages,
+// probe): plain 16-byte loads 16.8 us, non-temporal 15.6; LDS DMA 16.1,
+// non-temporal DMA 14.2. The prefill, whose K/V tiles several workgroups
+// read, keeps the plain forms.
+__device__ __forceinline__ void dma16_nt(const void* src, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+template <typename T>
+__device__ __forceinline__ T load_nt16(const void* p) {
+  static_assert(sizeof(T) == 16, "16-byte loads");
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(T, __builtin_nontemporal_load(static_cast<const u32x4*>(p)));
+}
+
 // Max and sum over the 4 lane groups of a 16-column tile (lanes r, r+16, r+32,
 // r+48), on gfx950's VALU lane swaps instead of LDS-routed shuffles. With the
 // same value in both registers, v_permlane32_swap leaves each lane holding its
