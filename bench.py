@@ -735,7 +735,9 @@ def _probe_lib():
     lib = ctypes.CDLL(path)
     vp, i = ctypes.c_void_p, ctypes.c_int
     lib.ie_probe_read.argtypes = [vp, ctypes.c_size_t, i, vp, vp]
+    lib.ie_probe_read_nt.argtypes = [vp, ctypes.c_size_t, i, vp, vp]
     lib.ie_probe_pages.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, vp, vp]
+    lib.ie_probe_pages_nt.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, vp, vp]
     return lib
 
 
@@ -747,7 +749,9 @@ def hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct
       read_256MB  the same for 256 MB over 4 buffers (1 GB): the large-stream rate;
       page_walk   config 3's own grid and block tables over the same rotated pools,
                   reading every K and V page of every (row, chunk) and nothing else.
-    ceiling_gbs is read_70MB: what one 70 MB read of this device achieves per launch."""
+    Each is timed with plain and with non-temporal loads (the form the decode kernel
+    reads its pages with) and reports the faster (`*_form`). ceiling_gbs is read_70MB:
+    what one 70 MB read of this device achieves per launch."""
     lib = _probe_lib()
     if lib is None:
         return None
@@ -762,19 +766,20 @@ def hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct
                 for _ in range(nbuf)]
 
         best = None
-        for per_cu in (4, 8, 16, 32):  # workgroups of 256 threads per compute unit
-            def step(i, bufs=bufs, nbytes=nbytes, nbuf=nbuf, wgs=per_cu * cus):
-                rc = lib.ie_probe_read(bufs[i % nbuf].data_ptr(), nbytes, wgs, sink.data_ptr(),
-                                       sp())
-                assert rc == 0
+        for form, fn in (("plain", lib.ie_probe_read), ("nontemporal", lib.ie_probe_read_nt)):
+            for per_cu in (4, 8, 16, 32):  # workgroups of 256 threads per compute unit
+                def step(i, bufs=bufs, nbytes=nbytes, nbuf=nbuf, wgs=per_cu * cus, fn=fn):
+                    rc = fn(bufs[i % nbuf].data_ptr(), nbytes, wgs, sink.data_ptr(), sp())
+                    assert rc == 0
 
-            ms = time_steps(torch, step, max(args.steps, 40), 5, stream)
-            if best is None or ms < best[0]:
-                best = (ms, per_cu)
+                ms = time_steps(torch, step, max(args.steps, 40), 5, stream)
+                if best is None or ms < best[0]:
+                    best = (ms, per_cu, form)
         ms = best[0]
         out[f"read_{mb}MB_gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         out[f"read_{mb}MB_us"] = round(ms * 1e3, 3)
         out[f"read_{mb}MB_workgroups_per_cu"] = best[1]
+        out[f"read_{mb}MB_form"] = best[2]
         del bufs
     rows, chunks = [], []
     for r, L in enumerate(lens):
@@ -787,16 +792,22 @@ def hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct
     page_bytes = PAGE * KVD * KV_BYTES[kv]
     walk_bytes = 2 * page_bytes * sum((int(L) + PAGE - 1) // PAGE for L in lens)
 
-    def walk(i):
-        l = i % len(k_pools)
-        rc = lib.ie_probe_pages(k_pools[l].data_ptr(), v_pools[l].data_ptr(), d_tab.data_ptr(),
-                                d_r.data_ptr(), d_c.data_ptr(), d_len.data_ptr(), len(rows),
-                                max_pages, ct, page_bytes, sink.data_ptr(), sp())
-        assert rc == 0
+    best = None
+    for form, fn in (("plain", lib.ie_probe_pages), ("nontemporal", lib.ie_probe_pages_nt)):
+        def walk(i, fn=fn):
+            l = i % len(k_pools)
+            rc = fn(k_pools[l].data_ptr(), v_pools[l].data_ptr(), d_tab.data_ptr(),
+                    d_r.data_ptr(), d_c.data_ptr(), d_len.data_ptr(), len(rows), max_pages, ct,
+                    page_bytes, sink.data_ptr(), sp())
+            assert rc == 0
 
-    ms = time_steps(torch, walk, max(args.steps, 40), 5, stream)
+        ms = time_steps(torch, walk, max(args.steps, 40), 5, stream)
+        if best is None or ms < best[0]:
+            best = (ms, form)
+    ms = best[0]
     out["page_walk_gbs"] = round(walk_bytes / (ms * 1e-3) / 1e9, 1)
     out["page_walk_us"] = round(ms * 1e3, 3)
+    out["page_walk_form"] = best[1]
     out["page_walk_bytes"] = walk_bytes
     out["ceiling_gbs"] = out["read_70MB_gbs"]
     return out
