@@ -66,12 +66,6 @@ struct Kv<IE_KV_F32> {
   __device__ __forceinline__ static void store4(elem* p, const float* x) {
     *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
   }
-  // With the non-temporal hint: page rows written once and not read again in
-  // the same launch (the append).
-  __device__ __forceinline__ static void store4_nt(elem* p, const float* x) {
-    typedef float f32x4v __attribute__((ext_vector_type(4)));
-    __builtin_nontemporal_store(f32x4v{x[0], x[1], x[2], x[3]}, reinterpret_cast<f32x4v*>(p));
-  }
   __device__ __forceinline__ static float load1(const elem* p) { return *p; }
 };
 
@@ -98,11 +92,6 @@ struct Kv16 {
     u.x = narrow(x[0]) | (narrow(x[1]) << 16);
     u.y = narrow(x[2]) | (narrow(x[3]) << 16);
     *reinterpret_cast<uint2*>(p) = u;
-  }
-  __device__ __forceinline__ static void store4_nt(elem* p, const float* x) {
-    typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
-    const u32x2v u = {narrow(x[0]) | (narrow(x[1]) << 16), narrow(x[2]) | (narrow(x[3]) << 16)};
-    __builtin_nontemporal_store(u, reinterpret_cast<u32x2v*>(p));
   }
   __device__ __forceinline__ static float load1(const elem* p) { return widen(*p); }
 };
