@@ -735,9 +735,9 @@ def _probe_lib():
     lib = ctypes.CDLL(path)
     vp, i = ctypes.c_void_p, ctypes.c_int
     lib.ie_probe_read.argtypes = [vp, ctypes.c_size_t, i, vp, vp]
-    lib.ie_probe_read_nt.argtypes = [vp, ctypes.c_size_t, i, vp, vp]
+    lib.ie_probe_read_form.argtypes = [vp, ctypes.c_size_t, i, i, vp, vp]
     lib.ie_probe_pages.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, vp, vp]
-    lib.ie_probe_pages_nt.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, vp, vp]
+    lib.ie_probe_pages_form.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, vp]
     return lib
 
 
@@ -749,9 +749,10 @@ def hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct
       read_256MB  the same for 256 MB over 4 buffers (1 GB): the large-stream rate;
       page_walk   config 3's own grid and block tables over the same rotated pools,
                   reading every K and V page of every (row, chunk) and nothing else.
-    Each is timed with plain and with non-temporal loads (the form the decode kernel
-    reads its pages with) and reports the faster (`*_form`). ceiling_gbs is read_70MB:
-    what one 70 MB read of this device achieves per launch."""
+    Each is timed in four load forms -- 16-byte loads into registers, plain or
+    non-temporal, and LDS DMA, plain or non-temporal (the decode kernel reads K pages
+    the second way and V pages the fourth) -- and reports the fastest (`*_form`).
+    ceiling_gbs is read_70MB: what one 70 MB read of this device achieves per launch."""
     lib = _probe_lib()
     if lib is None:
         return None
@@ -760,16 +761,18 @@ def hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct
     sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
     sp = lambda: torch.cuda.current_stream().cuda_stream  # the capture stream while recording
     out = {}
+    forms = ("plain", "nontemporal", "dma", "dma_nontemporal")
     for mb, nbuf in ((70, 8), (256, 4)):
-        nbytes = mb * 1000 * 1000 // 16 * 16
+        nbytes = mb * 1000 * 1000 // 4096 * 4096  # whole 4 KB blocks for the DMA forms
         bufs = [torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=dev)
                 for _ in range(nbuf)]
 
         best = None
-        for form, fn in (("plain", lib.ie_probe_read), ("nontemporal", lib.ie_probe_read_nt)):
+        for fi, form in enumerate(forms):
             for per_cu in (4, 8, 16, 32):  # workgroups of 256 threads per compute unit
-                def step(i, bufs=bufs, nbytes=nbytes, nbuf=nbuf, wgs=per_cu * cus, fn=fn):
-                    rc = fn(bufs[i % nbuf].data_ptr(), nbytes, wgs, sink.data_ptr(), sp())
+                def step(i, bufs=bufs, nbytes=nbytes, nbuf=nbuf, wgs=per_cu * cus, fi=fi):
+                    rc = lib.ie_probe_read_form(bufs[i % nbuf].data_ptr(), nbytes, wgs, fi,
+                                                sink.data_ptr(), sp())
                     assert rc == 0
 
                 ms = time_steps(torch, step, max(args.steps, 40), 5, stream)
@@ -793,12 +796,13 @@ def hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct
     walk_bytes = 2 * page_bytes * sum((int(L) + PAGE - 1) // PAGE for L in lens)
 
     best = None
-    for form, fn in (("plain", lib.ie_probe_pages), ("nontemporal", lib.ie_probe_pages_nt)):
-        def walk(i, fn=fn):
+    for fi, form in enumerate(forms):
+        def walk(i, fi=fi):
             l = i % len(k_pools)
-            rc = fn(k_pools[l].data_ptr(), v_pools[l].data_ptr(), d_tab.data_ptr(),
-                    d_r.data_ptr(), d_c.data_ptr(), d_len.data_ptr(), len(rows), max_pages, ct,
-                    page_bytes, sink.data_ptr(), sp())
+            rc = lib.ie_probe_pages_form(k_pools[l].data_ptr(), v_pools[l].data_ptr(),
+                                         d_tab.data_ptr(), d_r.data_ptr(), d_c.data_ptr(),
+                                         d_len.data_ptr(), len(rows), max_pages, ct, page_bytes,
+                                         fi, sink.data_ptr(), sp())
             assert rc == 0
 
         ms = time_steps(torch, walk, max(args.steps, 40), 5, stream)

@@ -9,8 +9,10 @@
 // stored only when it equals a value the data never produces, so the loads
 // stay and the stores do not count.
 //
-// Each comes in two load forms: plain, and with the non-temporal hint (the
-// form the decode kernels use for their pages); the bench takes the faster.
+// Each comes in four load forms: 16-byte loads into registers, plain or with
+// the non-temporal hint, and LDS DMA (global_load_lds_dwordx4: 1 KB per wave
+// instruction straight into LDS, the form the decode kernels read V pages
+// with), plain or non-temporal; the bench takes the fastest.
 //
 // ie_probe_pages: the decode kernel's access pattern without its arithmetic.
 // One workgroup per (row, chunk of chunk_tokens positions) of a batch in block
@@ -27,6 +29,27 @@ namespace {
 constexpr int kThreads = 256;
 
 __device__ __forceinline__ uint32_t fold(uint4 a) { return a.x ^ (a.y * 3u) ^ (a.z * 5u) ^ (a.w * 7u); }
+
+// One wave instruction moving 1 KB from src (lane l: bytes 16 l ..) to LDS
+// address lds (lane l lands at lds + 16 l).
+template <bool NT>
+__device__ __forceinline__ void dma_1k(const void* src, unsigned lds) {
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ unsigned lds_base(const void* p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p))));
+}
 
 template <bool NT>
 __device__ __forceinline__ uint4 load16(const void* p) {
@@ -51,6 +74,28 @@ probe_read_kernel(const uint4* __restrict__ src, size_t n16, uint32_t* __restric
     acc ^= fold(a) ^ fold(b) ^ fold(c) ^ fold(d);
   }
   for (; i < n16; i += stride) acc ^= fold(load16<NT>(src + i));
+  if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
+// The contiguous stream by LDS DMA: each wave moves 4 KB blocks (4 x 1 KB)
+// into its own LDS area, grid-stride over the blocks, one block in flight, and
+// folds one word of each so that the loads stay.
+template <bool NT>
+__global__ void __launch_bounds__(kThreads)
+probe_read_dma_kernel(const unsigned char* __restrict__ src, size_t blocks,
+                      uint32_t* __restrict__ sink) {
+  __shared__ __align__(16) unsigned char buf[kThreads / 64][4096];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const unsigned base = lds_base(&buf[wave][0]);
+  uint32_t acc = 0;
+  for (size_t b = size_t(blockIdx.x) * (kThreads / 64) + wave; b < blocks;
+       b += size_t(gridDim.x) * (kThreads / 64)) {
+    const unsigned char* p = src + b * 4096 + lane * 16;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dma_1k<NT>(p + u * 1024, base + u * 1024);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    acc ^= fold(*reinterpret_cast<const uint4*>(&buf[wave][lane * 16]));
+  }
   if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
 }
 
@@ -89,6 +134,38 @@ probe_pages_kernel(const unsigned char* __restrict__ k_pool, const unsigned char
   if (acc == 0x9E3779B9u) sink[w] = acc;
 }
 
+// The same walk by LDS DMA: wave w of the workgroup moves pages w, w + 4, ...
+// of the chunk, K then V (page_bytes / 1 KB instructions each), one page in
+// flight per wave.
+template <bool NT>
+__global__ void __launch_bounds__(kThreads)
+probe_pages_dma_kernel(const unsigned char* __restrict__ k_pool,
+                       const unsigned char* __restrict__ v_pool, const int32_t* __restrict__ tables,
+                       const int32_t* __restrict__ work_row, const int32_t* __restrict__ work_chunk,
+                       const int32_t* __restrict__ row_len, int max_pages, int chunk_tokens,
+                       int page_bytes, uint32_t* __restrict__ sink) {
+  extern __shared__ __align__(16) unsigned char dbuf[];  // [4 waves][2 pools][page_bytes]
+  const int w = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = work_row[w], c = work_chunk[w];
+  const int len = row_len[row];
+  const int p0 = c * chunk_tokens / 16;
+  const int np = (min((c + 1) * chunk_tokens, len) - c * chunk_tokens + 15) / 16;
+  const int32_t* tab = tables + size_t(row) * max_pages + p0;
+  unsigned char* mine = dbuf + size_t(wave) * 2 * page_bytes;
+  const unsigned base = lds_base(mine);
+  const int per = page_bytes / 1024;
+  uint32_t acc = 0;
+  for (int pg = wave; pg < np; pg += kThreads / 64) {
+    const size_t off = size_t(tab[pg]) * page_bytes + lane * 16;
+    for (int u = 0; u < per; ++u) dma_1k<NT>(k_pool + off + u * 1024, base + u * 1024);
+    for (int u = 0; u < per; ++u) dma_1k<NT>(v_pool + off + u * 1024, base + page_bytes + u * 1024);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    acc ^= fold(*reinterpret_cast<const uint4*>(mine + lane * 16)) ^
+           fold(*reinterpret_cast<const uint4*>(mine + page_bytes + lane * 16));
+  }
+  if (acc == 0x9E3779B9u) sink[w] = acc;
+}
+
 template <bool NT>
 int probe_pages(const void* k_pool, const void* v_pool, const int32_t* tables,
                        const int32_t* work_row, const int32_t* work_chunk, const int32_t* row_len,
@@ -116,17 +193,28 @@ int ie_probe_read(const void* src, size_t bytes, int workgroups, uint32_t* sink,
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-// The same with non-temporal loads.
-int ie_probe_read_nt(const void* src, size_t bytes, int workgroups, uint32_t* sink,
-                     hipStream_t stream) {
-  if (!src || !sink || bytes % 16 || workgroups <= 0) return 1;
-  hipLaunchKernelGGL(probe_read_kernel<true>, dim3(workgroups), dim3(kThreads), 0, stream,
-                     static_cast<const uint4*>(src), bytes / 16, sink);
+// Forms: 0 plain loads, 1 non-temporal loads, 2 LDS DMA, 3 non-temporal LDS
+// DMA. The DMA forms read bytes / 4096 whole 4 KB blocks.
+int ie_probe_read_form(const void* src, size_t bytes, int workgroups, int form, uint32_t* sink,
+                       hipStream_t stream) {
+  if (!src || !sink || bytes % 16 || workgroups <= 0 || form < 0 || form > 3) return 1;
+  const dim3 g(workgroups), b(kThreads);
+  if (form == 0)
+    hipLaunchKernelGGL(probe_read_kernel<false>, g, b, 0, stream, static_cast<const uint4*>(src),
+                       bytes / 16, sink);
+  else if (form == 1)
+    hipLaunchKernelGGL(probe_read_kernel<true>, g, b, 0, stream, static_cast<const uint4*>(src),
+                       bytes / 16, sink);
+  else if (form == 2)
+    hipLaunchKernelGGL(probe_read_dma_kernel<false>, g, b, 0, stream,
+                       static_cast<const unsigned char*>(src), bytes / 4096, sink);
+  else
+    hipLaunchKernelGGL(probe_read_dma_kernel<true>, g, b, 0, stream,
+                       static_cast<const unsigned char*>(src), bytes / 4096, sink);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-// The page walk of a flash-decoding launch of `items` (row, chunk) workgroups;
-// ie_probe_pages_nt with non-temporal loads.
+// The page walk of a flash-decoding launch of `items` (row, chunk) workgroups.
 int ie_probe_pages(const void* k_pool, const void* v_pool, const int32_t* tables,
                    const int32_t* work_row, const int32_t* work_chunk, const int32_t* row_len,
                    int items, int max_pages, int chunk_tokens, int page_bytes, uint32_t* sink,
@@ -134,12 +222,28 @@ int ie_probe_pages(const void* k_pool, const void* v_pool, const int32_t* tables
   return probe_pages<false>(k_pool, v_pool, tables, work_row, work_chunk, row_len, items,
                             max_pages, chunk_tokens, page_bytes, sink, stream);
 }
-int ie_probe_pages_nt(const void* k_pool, const void* v_pool, const int32_t* tables,
-                      const int32_t* work_row, const int32_t* work_chunk, const int32_t* row_len,
-                      int items, int max_pages, int chunk_tokens, int page_bytes, uint32_t* sink,
-                      hipStream_t stream) {
-  return probe_pages<true>(k_pool, v_pool, tables, work_row, work_chunk, row_len, items,
-                           max_pages, chunk_tokens, page_bytes, sink, stream);
+// Forms as for ie_probe_read_form; the DMA forms need page_bytes % 1024 == 0
+// (8 KB of LDS per page and wave, at most 8 KB pages).
+int ie_probe_pages_form(const void* k_pool, const void* v_pool, const int32_t* tables,
+                        const int32_t* work_row, const int32_t* work_chunk, const int32_t* row_len,
+                        int items, int max_pages, int chunk_tokens, int page_bytes, int form,
+                        uint32_t* sink, hipStream_t stream) {
+  if (form == 0 || form == 1)
+    return form ? probe_pages<true>(k_pool, v_pool, tables, work_row, work_chunk, row_len, items,
+                                    max_pages, chunk_tokens, page_bytes, sink, stream)
+                : probe_pages<false>(k_pool, v_pool, tables, work_row, work_chunk, row_len, items,
+                                     max_pages, chunk_tokens, page_bytes, sink, stream);
+  if (form != 2 && form != 3) return 1;
+  if (!k_pool || !v_pool || !tables || items <= 0 || chunk_tokens % 16 || page_bytes % 1024 ||
+      page_bytes > 8192)
+    return 1;
+  const size_t lds = size_t(kThreads / 64) * 2 * page_bytes;
+  const auto kern = form == 3 ? probe_pages_dma_kernel<true> : probe_pages_dma_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3(items), dim3(kThreads), lds, stream,
+                     static_cast<const unsigned char*>(k_pool),
+                     static_cast<const unsigned char*>(v_pool), tables, work_row, work_chunk,
+                     row_len, max_pages, chunk_tokens, page_bytes, sink);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
 }  // extern "C"
