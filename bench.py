@@ -967,11 +967,10 @@ def bench_model(args, torch, ie, O):
     """Config 6: the whole decode step around the path -- a 24-layer Qwen2.5-0.5B decoder
     (hidden 896, intermediate 4,864, 14/2 heads, tied LM head over 151,936 tokens) with
     random BF16 weights, one new token for each of config 3's 64 rows (L ~ U[128, 4096],
-    f16 KV, shuffled 16-token pages, one pool pair per layer). Per layer: rmsnorm,
-    q/k/v, RoPE + paged append + attention (one launch), o_proj into the residual,
-    rmsnorm, gate/up + SiLU, down into the residual (q/k/v in one launch); then the final
-    norm and the logits
-    of every row (src/cuda/cuda_runner.cu:418-470)."""
+    f16 KV, shuffled 16-token pages, one pool pair per layer). Per layer: rmsnorm folded
+    into q/k/v (one launch), RoPE + paged append + attention (one launch), o_proj into the
+    residual, rmsnorm folded into gate/up + SiLU (one launch), down into the residual;
+    then the final norm and the logits of every row (src/cuda/cuda_runner.cu:418-470)."""
     dev = torch.device("cuda:0")
     kv = args.kv or "f16"
     rng = np.random.default_rng(args.seed)
@@ -1048,13 +1047,11 @@ def bench_model(args, torch, ie, O):
         ie.embedding(x, ids, m_e)
         for l in range(layers):
             t, m = Wl[l], M[l]
-            ie.rmsnorm(xn, x, t["inorm"], eps)
-            ie.qkv_proj(q, k, v, xn, m["qkv"], t["bqkv"])
+            ie.rmsnorm_qkv_proj(q, k, v, x, t["inorm"], eps, m["qkv"], t["bqkv"])
             ie.rope_cache_attention(attn, q, k, v, k_pools[l], v_pools[l], table, d_pos, d_seq,
                                     tabs[l], max_pages, nc, ct, ws, NH, NKV, HD)
             ie.matmul(x, attn, m["o"], accumulate=True)
-            ie.rmsnorm(xn, x, t["pnorm"], eps)
-            ie.gate_up_silu(mid, xn, m["g"], m["u"])
+            ie.rmsnorm_gate_up_silu(mid, x, t["pnorm"], eps, m["g"], m["u"])
             ie.matmul(x, mid, m["d"], accumulate=True)
         ie.rmsnorm(xn, x, final_norm, eps)
         ie.matmul(logits, xn, m_e)
@@ -1072,8 +1069,8 @@ def bench_model(args, torch, ie, O):
         "value": round(B / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": kv, "data": "synthetic",
-        "config": {"workload": "config 6: 24 layers x (rmsnorm, q/k/v, RoPE+append+attention, "
-                               "o_proj, rmsnorm, gate/up+SiLU, down) + final norm + tied LM "
+        "config": {"workload": "config 6: 24 layers x (rmsnorm+q/k/v, RoPE+append+attention, "
+                               "o_proj, rmsnorm+gate/up+SiLU, down) + final norm + tied LM "
                                "head, batch 64, L~U[128,4096], random BF16 weights",
                    "kv_dtype": kv, "weights": args.weights, "chunk_tokens": ct,
                    "num_chunks": nc, "seed": args.seed},

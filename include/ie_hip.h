@@ -296,6 +296,22 @@ int ie_hip_qkv_proj(float* q, float* k, float* v, const float* x, ie_matrix w_qk
 int ie_hip_gate_up_silu(float* out, const float* x, ie_matrix w_gate, ie_matrix w_up, int T,
                         hipStream_t stream);
 
+/* The rmsnorm before a projection, folded into it: the same as
+ * ie_hip_rmsnorm(xn, x, norm_weight, T, cols, eps) followed by ie_hip_qkv_proj
+ * (or ie_hip_gate_up_silu) on xn, in one launch and without xn: y =
+ * (x * norm_weight) . W^T * (1 / sqrt(mean(x^2) + eps)), the sum of squares
+ * taken in an order that depends on the matrix shape only. Equal to the two
+ * calls to float32 rounding (the factors are applied in another order). For
+ * matrices below 16 row tiles per compute unit (the 0.5B layer's 1,152-row
+ * q/k/v and 4,864-row gate/up); norm_weight [cols], 16-byte aligned. No
+ * counterpart in the reference, which launches rmsnorm and then the
+ * projections (src/cuda/cuda_runner.cu:436-439,449-450). */
+int ie_hip_rmsnorm_qkv_proj(float* q, float* k, float* v, const float* x,
+                            const float* norm_weight, float eps, ie_matrix w_qkv,
+                            const float* b_qkv, int T, int q_dim, int kv_dim, hipStream_t stream);
+int ie_hip_rmsnorm_gate_up_silu(float* out, const float* x, const float* norm_weight, float eps,
+                                ie_matrix w_gate, ie_matrix w_up, int T, hipStream_t stream);
+
 /* out[r] = index of the maximum of logits[r, 0..n) for r < R: the greedy
  * token of each row, with the reference CPU argmax's semantics
  * (src/sampler.cpp:26-31): the first strict maximum in index order (ties go

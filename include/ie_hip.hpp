@@ -157,6 +157,17 @@ inline void gate_up_silu(float* out, const float* x, const ie_matrix& wg, const 
                          int T, hipStream_t stream) {
   check(ie_hip_gate_up_silu(out, x, wg, wu, T, stream));
 }
+/* rmsnorm folded into qkv_proj / gate_up_silu (no reference counterpart). */
+inline void rmsnorm_qkv_proj(float* q, float* k, float* v, const float* x, const float* norm,
+                             float eps, const ie_matrix& w_qkv, const float* b_qkv, int T,
+                             int q_dim, int kv_dim, hipStream_t stream) {
+  check(ie_hip_rmsnorm_qkv_proj(q, k, v, x, norm, eps, w_qkv, b_qkv, T, q_dim, kv_dim, stream));
+}
+inline void rmsnorm_gate_up_silu(float* out, const float* x, const float* norm, float eps,
+                                 const ie_matrix& wg, const ie_matrix& wu, int T,
+                                 hipStream_t stream) {
+  check(ie_hip_rmsnorm_gate_up_silu(out, x, norm, eps, wg, wu, T, stream));
+}
 
 /* gather_rows (kernels.cuh:101-102). */
 inline void gather_rows(float* dst, const float* src, const int* rows, int R, int dim,

@@ -4,9 +4,13 @@
  * (src/cuda/cuda_runner.cu:418-470):
  *   begin               x = E[ids]                               (embedding)
  *   per layer, around the engine's RoPE + paged append + attention:
- *     before_attention  xn = rmsnorm(x); q, k, v = xn . W^T + b  (one launch)
- *     after_attention   x += attn . Wo^T; xn = rmsnorm(x);
- *                       mid = silu(xn . Wg^T) * (xn . Wu^T); x += mid . Wd^T
+ *     before_attention  q, k, v = rmsnorm(x) . W^T + b          (one launch)
+ *     after_attention   x += attn . Wo^T;
+ *                       mid = silu(xn . Wg^T) * (xn . Wu^T), xn = rmsnorm(x)
+ *                                                                (one launch);
+ *                       x += mid . Wd^T
+ *   (each rmsnorm folded into the projection after it: ie_hip_rmsnorm_qkv_proj,
+ *   ie_hip_rmsnorm_gate_up_silu)
  *   end                 for the rows that want logits: xg = rmsnorm(x[rows]);
  *                       logits = xg . E_out^T
  * The rows that want logits are gathered before the final norm, which is the
@@ -218,15 +222,13 @@ class DecoderModel {
     };
     b.before_attention = [this, &engine](int l, int rows, hipStream_t s) {
       const Layer& L = layers_[l];
-      rmsnorm(xn_, x_, L.input_norm, rows, shape_.hidden, shape_.rms_eps, s);
-      qkv_proj(engine.q(), engine.k(), engine.v(), xn_, L.wqkv, L.bqkv, rows, kv_.q_dim(),
-               kv_.kv_dim(), s);
+      rmsnorm_qkv_proj(engine.q(), engine.k(), engine.v(), x_, L.input_norm, shape_.rms_eps,
+                       L.wqkv, L.bqkv, rows, kv_.q_dim(), kv_.kv_dim(), s);
     };
     b.after_attention = [this, &engine](int l, int rows, hipStream_t s) {
       const Layer& L = layers_[l];
       matmul(x_, engine.attn(), L.wo, nullptr, rows, true, s);
-      rmsnorm(xn_, x_, L.post_norm, rows, shape_.hidden, shape_.rms_eps, s);
-      gate_up_silu(mid_, xn_, L.w_gate, L.w_up, rows, s);
+      rmsnorm_gate_up_silu(mid_, x_, L.post_norm, shape_.rms_eps, L.w_gate, L.w_up, rows, s);
       matmul(x_, mid_, L.w_down, nullptr, rows, true, s);
     };
     b.end = [this, &engine](int rows, int n, hipStream_t s) {

@@ -86,6 +86,8 @@ _SIGS = {
     "ie_hip_matmul": (_i, [_vp, _vp, Matrix, _vp, _i, _i, _vp]),
     "ie_hip_gate_up_silu": (_i, [_vp, _vp, Matrix, Matrix, _i, _vp]),
     "ie_hip_qkv_proj": (_i, [_vp, _vp, _vp, _vp, Matrix, _vp, _i, _i, _i, _vp]),
+    "ie_hip_rmsnorm_qkv_proj": (_i, [_vp, _vp, _vp, _vp, _vp, _f, Matrix, _vp, _i, _i, _i, _vp]),
+    "ie_hip_rmsnorm_gate_up_silu": (_i, [_vp, _vp, _vp, _f, Matrix, Matrix, _i, _vp]),
     "ie_pages_create": (_vp, [_i, _i, _i]),
     "ie_pages_destroy": (None, [_vp]),
     "ie_pages_open_sequence": (_i, [_vp]),
@@ -368,6 +370,22 @@ def gate_up_silu(out, x, w_gate: Matrix, w_up: Matrix, stream=None) -> None:
     """out = silu(x . Wg^T) * (x . Wu^T) (src/cuda/kernels.cuh:64-66)."""
     _check(lib().ie_hip_gate_up_silu(_ptr(out), _ptr(x), w_gate, w_up, x.numel() // w_gate.cols,
                                      _stream(stream)))
+
+
+def rmsnorm_qkv_proj(q, k, v, x, norm, eps: float, w_qkv: Matrix, b_qkv=None,
+                     stream=None) -> None:
+    """qkv_proj(rmsnorm(x, norm, eps)) in one launch (no reference counterpart)."""
+    q_dim, kv_dim = q.shape[-1], k.shape[-1]
+    _check(lib().ie_hip_rmsnorm_qkv_proj(_ptr(q), _ptr(k), _ptr(v), _ptr(x), _ptr(norm), eps,
+                                         w_qkv, _ptr(b_qkv), x.numel() // w_qkv.cols, q_dim,
+                                         kv_dim, _stream(stream)))
+
+
+def rmsnorm_gate_up_silu(out, x, norm, eps: float, w_gate: Matrix, w_up: Matrix,
+                         stream=None) -> None:
+    """gate_up_silu(rmsnorm(x, norm, eps)) in one launch (no reference counterpart)."""
+    _check(lib().ie_hip_rmsnorm_gate_up_silu(_ptr(out), _ptr(x), _ptr(norm), eps, w_gate, w_up,
+                                             x.numel() // w_gate.cols, _stream(stream)))
 
 
 def gather_kv(dst, pool, tables, max_pages: int, seq: int, length: int, kv_dim: int,

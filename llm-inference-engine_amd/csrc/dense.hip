@@ -90,15 +90,27 @@ struct RowSplit {
   int split0, split1;
 };
 
-template <bool GATE, int RT, int TT, int W, bool I8>
+// NORM: the rmsnorm before the matmul, folded into it (the decode step's
+// xn = rmsnorm(x); y = xn . W^T pairs). y = (x * w_norm) . W^T * inv_rms(x):
+// the activations are scaled by the norm weight as they are split, each lane
+// sums the squares of the raw x it loads, the waves add those sums through LDS
+// in the same fixed tree as their tiles, and the epilogue takes the row's
+// 1 / sqrt(mean(x^2) + eps). The orders depend on the matrix shape alone.
+struct RowNorm {
+  const float* weight;  // [cols]
+  float eps;
+};
+
+template <bool GATE, int RT, int TT, int W, bool I8, bool NORM = false>
 __global__ void __launch_bounds__(64 * W)
 matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const void* __restrict__ w,
                    const float* __restrict__ scale, const void* __restrict__ w2,
                    const float* __restrict__ scale2, const float* __restrict__ bias,
-                   int T, int rows, int cols, int accumulate, RowSplit out) {
+                   int T, int rows, int cols, int accumulate, RowSplit out, RowNorm norm) {
   constexpr int NA = GATE ? 2 : 1, NT = NA * RT * TT;
   static_assert(NT <= 16, "at most 16 accumulator tiles (64 KB of LDS for the reduction)");
   __shared__ f32x4 red[W / 2][NT][64];
+  __shared__ float red_ss[NORM ? W / 2 : 1][TT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int row0 = blockIdx.x * 16 * RT, tok0 = blockIdx.y * 16 * TT;
@@ -115,9 +127,19 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
     for (int i = 0; i < RT; ++i)
 #pragma unroll
       for (int j = 0; j < TT; ++j) acc[n][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ss[TT];  // NORM: this lane's sum of x^2 of its token (row r of token tile j)
+#pragma unroll
+  for (int j = 0; j < TT; ++j) ss[j] = 0.0f;
   for (int kb = 32 * wave; kb < cols; kb += 32 * W) {
     const int k = kb + 8 * g;
     const bool kin = k < cols;
+    float4 wn0 = make_float4(1.f, 1.f, 1.f, 1.f), wn1 = wn0;
+    if constexpr (NORM) {
+      if (kin) {
+        wn0 = *reinterpret_cast<const float4*>(norm.weight + k);
+        wn1 = *reinterpret_cast<const float4*>(norm.weight + k + 4);
+      }
+    }
     bf16x8 a[NA][RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
@@ -129,13 +151,27 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
       bf16x8 bh = {}, bm = {}, bl = {};
       if (kin) {
         const float4* xp = reinterpret_cast<const float4*>(xrow[j] + k);
-        split3(xp[0], xp[1], bh, bm, bl);
+        float4 x0 = xp[0], x1 = xp[1];
+        if constexpr (NORM) {
+          const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss[j] = __builtin_fmaf(v[e], v[e], ss[j]);
+          x0 = make_float4(x0.x * wn0.x, x0.y * wn0.y, x0.z * wn0.z, x0.w * wn0.w);
+          x1 = make_float4(x1.x * wn1.x, x1.y * wn1.y, x1.z * wn1.z, x1.w * wn1.w);
+        }
+        split3(x0, x1, bh, bm, bl);
       }
 #pragma unroll
       for (int n = 0; n < NA; ++n)
 #pragma unroll
         for (int i = 0; i < RT; ++i) acc[n][i][j] = mma3(a[n][i], bh, bm, bl, acc[n][i][j]);
     }
+  }
+  // NORM: the token's sum over the 4 lane groups of its K slices (lanes r,
+  // r + 16, r + 32, r + 48), then with the tiles through the waves' tree.
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < TT; ++j) ss[j] = group_sum4(ss[j]);
   }
   // The waves' partial tiles summed through LDS in a fixed tree (waves 4-7
   // into 0-3, 2-3 into 0-1, 1 into 0), so results do not depend on timing.
@@ -148,6 +184,10 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
         for (int i = 0; i < RT; ++i)
 #pragma unroll
           for (int j = 0; j < TT; ++j) red[wave - half][(n * RT + i) * TT + j][lane] = acc[n][i][j];
+      if constexpr (NORM) {
+#pragma unroll
+        for (int j = 0; j < TT; ++j) red_ss[wave - half][j][lane] = ss[j];
+      }
     }
     __syncthreads();
     if (wave < half) {
@@ -157,6 +197,10 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
         for (int i = 0; i < RT; ++i)
 #pragma unroll
           for (int j = 0; j < TT; ++j) acc[n][i][j] += red[wave][(n * RT + i) * TT + j][lane];
+      if constexpr (NORM) {
+#pragma unroll
+        for (int j = 0; j < TT; ++j) ss[j] += red_ss[wave][j][lane];
+      }
     }
     __syncthreads();
   }
@@ -165,6 +209,8 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
   for (int j = 0; j < TT; ++j) {
     const int tok = tok0 + 16 * j + r;
     if (tok >= T) break;
+    // NORM: the token's 1 / rms (1 otherwise)
+    const float inv = NORM ? 1.0f / sqrtf(ss[j] / float(cols) + norm.eps) : 1.0f;
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
 #pragma unroll
@@ -172,6 +218,7 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
         const int row = row0 + 16 * i + 4 * g + e;
         if (row >= rows) break;
         float v = acc[0][i][j][e] * (I8 ? scale[row] : 1.0f);
+        if constexpr (NORM) v *= inv;
         float* dst;
         if (row < out.split0)
           dst = y + size_t(tok) * out.split0 + row;
@@ -180,7 +227,9 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
         else
           dst = out.y2 + size_t(tok) * (rows - out.split1) + (row - out.split1);
         if constexpr (GATE) {
-          v = silu(v) * (acc[NA - 1][i][j][e] * (I8 ? scale2[row] : 1.0f));
+          float u = acc[NA - 1][i][j][e] * (I8 ? scale2[row] : 1.0f);
+          if constexpr (NORM) u *= inv;
+          v = silu(v) * u;
         } else {
           if (bias) v += bias[row];
           if (accumulate) v += *dst;
@@ -257,7 +306,8 @@ int check_matrix(const ie_matrix& m, const char* who) {
 
 int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const ie_matrix* w2,
                   const float* bias, int T, int accumulate, hipStream_t stream, const char* who,
-                  RowSplit split = RowSplit{nullptr, nullptr, 0, 0}) {
+                  RowSplit split = RowSplit{nullptr, nullptr, 0, 0},
+                  RowNorm norm = RowNorm{nullptr, 0.0f}) {
   if (split.split0 == 0 && split.split1 == 0) split.split0 = split.split1 = w.rows;
   if (int rc = check_matrix(w, who)) return rc;
   if (w2) {
@@ -301,14 +351,45 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   if (grid.y > 65535) return fail(IE_HIP_EINVAL, std::string(who) + ": too many tokens");
   const void* w2d = gate ? w2->data : nullptr;
   const float* s2 = gate ? w2->scale : nullptr;
+  if (norm.weight) {
+    // The folded rmsnorm exists for the 8-wave, one-token-tile launches (every
+    // matrix below 16 row tiles per compute unit).
+    if (wide) return fail(IE_HIP_EINVAL, std::string(who) + ": too many rows for the folded rmsnorm");
+#define IE_MM_NORM(G, R)                                                                          \
+  do {                                                                                            \
+    if (w.int8)                                                                                   \
+      hipLaunchKernelGGL((matmul_mfma_kernel<G, R, 1, kMmWaves, true, true>), grid, block, 0,     \
+                         stream, y, x, w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols,         \
+                         accumulate, split, norm);                                                \
+    else                                                                                          \
+      hipLaunchKernelGGL((matmul_mfma_kernel<G, R, 1, kMmWaves, false, true>), grid, block, 0,    \
+                         stream, y, x, w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols,         \
+                         accumulate, split, norm);                                                \
+  } while (0)
+    if (gate) {
+      if (RT == 2)
+        IE_MM_NORM(true, 2);
+      else
+        IE_MM_NORM(true, 1);
+    } else {
+      if (RT == 2)
+        IE_MM_NORM(false, 2);
+      else
+        IE_MM_NORM(false, 1);
+    }
+#undef IE_MM_NORM
+    return check_launch(who);
+  }
 #define IE_MM_LAUNCH_W(G, R, C, W)                                                               \
   do {                                                                                           \
     if (w.int8)                                                                                  \
       hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C, W, true>), grid, block, 0, stream, y, x,   \
-                         w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols, accumulate, split);  \
+                         w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols, accumulate, split,   \
+                         norm);                                                                  \
     else                                                                                         \
       hipLaunchKernelGGL((matmul_mfma_kernel<G, R, C, W, false>), grid, block, 0, stream, y, x,  \
-                         w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols, accumulate, split);  \
+                         w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols, accumulate, split,   \
+                         norm);                                                                  \
   } while (0)
 #define IE_MM_LAUNCH(G, R, C)            \
   do {                                   \
@@ -391,4 +472,30 @@ extern "C" int ie_hip_gate_up_silu(float* out, const float* x, ie_matrix w_gate,
                                    int T, hipStream_t stream) {
   clear_error();
   return launch_matmul(true, out, x, w_gate, &w_up, nullptr, T, 0, stream, "gate_up_silu");
+}
+
+extern "C" int ie_hip_rmsnorm_qkv_proj(float* q, float* k, float* v, const float* x,
+                                       const float* norm_weight, float eps, ie_matrix w_qkv,
+                                       const float* b_qkv, int T, int q_dim, int kv_dim,
+                                       hipStream_t stream) {
+  clear_error();
+  if (q_dim <= 0 || kv_dim <= 0 || w_qkv.rows != q_dim + 2 * kv_dim)
+    return fail(IE_HIP_EINVAL, "rmsnorm_qkv_proj: weight rows must be q_dim + 2 kv_dim");
+  if (T > 0 && (!q || !k || !v || !norm_weight))
+    return fail(IE_HIP_EINVAL, "rmsnorm_qkv_proj: null pointer");
+  if (reinterpret_cast<uintptr_t>(norm_weight) & 15)
+    return fail(IE_HIP_EINVAL, "rmsnorm_qkv_proj: the norm weight must be 16-byte aligned");
+  return launch_matmul(false, q, x, w_qkv, nullptr, b_qkv, T, 0, stream, "rmsnorm_qkv_proj",
+                       RowSplit{k, v, q_dim, q_dim + kv_dim}, RowNorm{norm_weight, eps});
+}
+
+extern "C" int ie_hip_rmsnorm_gate_up_silu(float* out, const float* x, const float* norm_weight,
+                                           float eps, ie_matrix w_gate, ie_matrix w_up, int T,
+                                           hipStream_t stream) {
+  clear_error();
+  if (T > 0 && !norm_weight) return fail(IE_HIP_EINVAL, "rmsnorm_gate_up_silu: null pointer");
+  if (reinterpret_cast<uintptr_t>(norm_weight) & 15)
+    return fail(IE_HIP_EINVAL, "rmsnorm_gate_up_silu: the norm weight must be 16-byte aligned");
+  return launch_matmul(true, out, x, w_gate, &w_up, nullptr, T, 0, stream, "rmsnorm_gate_up_silu",
+                       RowSplit{nullptr, nullptr, 0, 0}, RowNorm{norm_weight, eps});
 }

@@ -145,6 +145,98 @@ def test_qkv_proj_matches_three_matmuls(ie, dev, int8, T):
     assert rel_err(v.cpu().numpy(), want[:, QD + KVD:]) <= REL
 
 
+EPS = 1e-6
+
+
+@pytest.mark.parametrize("int8", [False, True])
+@pytest.mark.parametrize("T", [1, 64, 300])
+def test_rmsnorm_qkv_proj(ie, dev, int8, T):
+    """The input norm folded into the q/k/v projection: against the oracle's rmsnorm
+    followed by the projection (the reference's two launches)."""
+    rng = np.random.default_rng(40 + T)
+    H, QD, KVD = 896, 896, 128
+    x = rng.standard_normal((T, H), dtype=np.float32) * np.float32(4.0)
+    wn = rng.standard_normal(H, dtype=np.float32)
+    w32 = rng.standard_normal((QD + 2 * KVD, H), dtype=np.float32) * np.float32(0.05)
+    b = rng.standard_normal(QD + 2 * KVD, dtype=np.float32)
+    m, keep, (w, fmt, s) = dev_weights(ie, dev, w32, int8)
+    q = torch.full((T, QD), float("nan"), device=dev)
+    k = torch.full((T, KVD), float("nan"), device=dev)
+    v = torch.full((T, KVD), float("nan"), device=dev)
+    ie.rmsnorm_qkv_proj(q, k, v, torch.from_numpy(x).to(dev), torch.from_numpy(wn).to(dev), EPS,
+                        m, torch.from_numpy(b).to(dev))
+    torch.cuda.synchronize()
+    want = O.matmul(O.rmsnorm(x, wn, EPS), w, fmt, s, b)
+    assert rel_err(q.cpu().numpy(), want[:, :QD]) <= REL
+    assert rel_err(k.cpu().numpy(), want[:, QD:QD + KVD]) <= REL
+    assert rel_err(v.cpu().numpy(), want[:, QD + KVD:]) <= REL
+
+
+@pytest.mark.parametrize("int8", [False, True])
+@pytest.mark.parametrize("T", [1, 64, 1024])
+def test_rmsnorm_gate_up_silu(ie, dev, int8, T):
+    """The post-attention norm folded into gate/up + SiLU, against the oracle's rmsnorm
+    followed by the two projections and silu(g) * u."""
+    rng = np.random.default_rng(50 + T)
+    rows, cols = 4864, 896
+    x = rng.standard_normal((T, cols), dtype=np.float32) * np.float32(4.0)
+    wn = rng.standard_normal(cols, dtype=np.float32)
+    wg32 = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+    wu32 = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+    mg, kg, (wg, fmt, sg) = dev_weights(ie, dev, wg32, int8)
+    mu, ku, (wu, _, su) = dev_weights(ie, dev, wu32, int8)
+    out = torch.full((T, rows), float("nan"), device=dev)
+    ie.rmsnorm_gate_up_silu(out, torch.from_numpy(x).to(dev), torch.from_numpy(wn).to(dev), EPS,
+                            mg, mu)
+    torch.cuda.synchronize()
+    xn = O.rmsnorm(x, wn, EPS)
+    want = O.silu_mul(O.matmul(xn, wg, fmt, sg), O.matmul(xn, wu, fmt, su))
+    assert rel_err(out.cpu().numpy(), want) <= REL
+
+
+def test_rmsnorm_folds_batch_invariant(ie, dev):
+    """A row's output is the same bits in a batch of 64 as alone (the sum of squares is
+    reduced in an order fixed by the matrix shape)."""
+    rng = np.random.default_rng(60)
+    H, QD, KVD, rows = 896, 896, 128, 4864
+    x = rng.standard_normal((64, H), dtype=np.float32) * np.float32(4.0)
+    wn = torch.from_numpy(rng.standard_normal(H, dtype=np.float32)).to(dev)
+    m, keep, _ = dev_weights(ie, dev, rng.standard_normal((QD + 2 * KVD, H), dtype=np.float32) *
+                            np.float32(0.05), False)
+    mg, kg, _ = dev_weights(ie, dev, rng.standard_normal((rows, H), dtype=np.float32) *
+                            np.float32(0.05), False)
+    mu, ku, _ = dev_weights(ie, dev, rng.standard_normal((rows, H), dtype=np.float32) *
+                            np.float32(0.05), False)
+
+    def run(xs):
+        T = xs.shape[0]
+        q, k, v = (torch.empty((T, n), device=dev) for n in (QD, KVD, KVD))
+        g = torch.empty((T, rows), device=dev)
+        dx = torch.from_numpy(np.ascontiguousarray(xs)).to(dev)
+        ie.rmsnorm_qkv_proj(q, k, v, dx, wn, EPS, m)
+        ie.rmsnorm_gate_up_silu(g, dx, wn, EPS, mg, mu)
+        torch.cuda.synchronize()
+        return [t.cpu().numpy() for t in (q, k, v, g)]
+
+    batch = run(x)
+    for t in (0, 17, 63):
+        alone = run(x[t:t + 1])
+        for b_, a_ in zip(batch, alone):
+            assert np.array_equal(b_[t:t + 1].view(np.uint32), a_.view(np.uint32)), t
+
+
+def test_rmsnorm_fold_errors(ie, dev):
+    x = torch.zeros((4, 896), device=dev)
+    w = torch.zeros((16, 896), dtype=torch.int16, device=dev)
+    q, k, v = (torch.zeros((4, n), device=dev) for n in (8, 4, 4))
+    with pytest.raises(ie.IeHipError, match="null pointer"):
+        ie.rmsnorm_qkv_proj(q, k, v, x, None, EPS, ie.matrix(w))
+    wn = torch.zeros(897, device=dev)[1:]  # 4-byte aligned only
+    with pytest.raises(ie.IeHipError, match="aligned"):
+        ie.rmsnorm_gate_up_silu(torch.zeros((4, 16), device=dev), x, wn, EPS, ie.matrix(w),
+                                ie.matrix(w))
+
+
 def test_dense_argument_errors(ie, dev):
     x = torch.zeros((4, 12), device=dev)
     y = torch.zeros((4, 16), device=dev)
