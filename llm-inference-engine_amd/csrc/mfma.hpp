@@ -193,6 +193,14 @@ __device__ __forceinline__ void split16x2<__bf16>(float x0, float x1, __bf16& h0
   split16(x1, h1, l1);
 }
 
+// Two f32 values as one packed f16 pair rounded toward zero (v_cvt_pkrtz_f16_f32):
+// |x - h| < 2^-10 |x| for normal results.
+__device__ __forceinline__ void round16x2_rtz(float x0, float x1, _Float16& h0, _Float16& h1) {
+  const unsigned hb = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+  h0 = __builtin_bit_cast(_Float16, static_cast<unsigned short>(hb));
+  h1 = __builtin_bit_cast(_Float16, static_cast<unsigned short>(hb >> 16));
+}
+
 // 2^x for the softmax weights: the bare v_exp_f32 (x <= 0 here; results below
 // 2^-126, where it may flush to zero, are far below the weights' tolerance).
 __device__ __forceinline__ float exp2_weight(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -17,10 +17,15 @@
 // online-softmax statistics of a row never leave its lanes except for the
 // reductions over the 4 lane groups.
 //
-// Precision: K and V enter exactly; q (pre-scaled by log2(e)/8) and P are split
-// into hi + lo halves of the same 16-bit type and each product is done twice --
-// float32-level scores and weights (the 2e-3 absolute bound for 16-bit caches
-// holds with a wide margin; measured errors are ~1e-6).
+// Precision: K and V enter exactly. With an f16 cache, q (pre-scaled by
+// log2(e)/8, rounded to nearest) and P (weights <= 2^kLazyMax, rounded toward
+// zero) enter as single f16 values -- the operand rounding of the reference's
+// tensor-core kernel (src/cuda/kernels.cu:673-674,741), here with the row sums
+// taken from the same rounded P on the matrix cores, so the output is a weighted
+// mean with weights off by < 2^-10 relative (errors ~6e-4 at 4,000 keys against
+// the 2e-3 absolute bound). bf16 keeps 8 mantissa bits, too few for that bound:
+// with a bf16 cache q and P are split into hi + lo halves and each product is
+// done twice (float32-level scores and weights, errors ~1e-6).
 //
 // Layout of the work:
 //   One workgroup per (pair of 16-row blocks, KV head); one wave per query head
@@ -46,6 +51,7 @@
 //   (-inf scores, and their V rows zeroed in LDS before use, so stale or
 //   non-finite memory cannot reach the output through 0 * x).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "mfma.hpp"
@@ -79,6 +85,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
+  constexpr bool kSplit = !std::is_same_v<E, _Float16>;  // hi + lo operands (bf16)
   constexpr int kRingSteps = kTeams == 1 ? 4 : 3;  // steps of kTeams tiles in LDS
   constexpr int kRingBytes = kRingSteps * kTeams * kBufBytes;
   op ones;  // all-ones A operand: row sums of P^T on the matrix cores
@@ -179,8 +186,8 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     const int min_pos = pos0 + t0;      // first row's position
     const int n_tiles = max_pos / kKeys + 1;
 
-    // Queries of row t0 + r for the wave's heads, times log2(e)/8, split hi + lo:
-    // the B operands of S^T (dims 32 ks + 8g .. +8).
+    // Queries of row t0 + r for the wave's heads, times log2(e)/8 (split hi + lo
+    // for bf16): the B operands of S^T (dims 32 ks + 8g .. +8).
     const int t = t0 + r;
     const bool row_ok = t < T;
     const int rp = pos0 + t;  // this lane's row position
@@ -205,8 +212,11 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
                             a[ks][1].x, a[ks][1].y, a[ks][1].z, a[ks][1].w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          E hv, lv;
-          split16(x[j] * qs, hv, lv);
+          E hv, lv = static_cast<E>(0.0f);
+          if constexpr (kSplit)
+            split16(x[j] * qs, hv, lv);
+          else
+            hv = static_cast<E>(x[j] * qs);
           qhi[hh][ks][j] = hv;
           qlo[hh][ks][j] = lv;
         }
@@ -316,7 +326,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
 #pragma unroll
               for (int ks = 0; ks < 2; ++ks) {
                 acc = M::mma(ka[kt4][ks], qhi[hh][ks], acc);
-                acc = M::mma(ka[kt4][ks], qlo[hh][ks], acc);
+                if constexpr (kSplit) acc = M::mma(ka[kt4][ks], qlo[hh][ks], acc);
               }
               s[hh][kt4] = acc;
             }
@@ -338,8 +348,9 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
           // 4g + e. The reference max m is raised lazily: weights are 2^(s - m) with
           // m the row's max when it was last raised, and O and l are rescaled only
           // when some row of the wave sees its max grow past m + kLazyMax (so weights
-          // stay below 2^kLazyMax, which the 16-bit hi + lo split carries at full
-          // precision). The row sums l come from the matrix cores (below).
+          // stay below 2^kLazyMax, in range for f16 and, split hi + lo, carried at
+          // full precision in bf16). The row sums l come from the matrix cores
+          // (below), from the same operands as O.
           op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
 #pragma unroll
           for (int hh = 0; hh < kHeadsPerWave; ++hh) {
@@ -374,23 +385,31 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
                 const float pb0 = exp2_weight(s[hh][2 * kg + 1][e]);
                 const float pb1 = exp2_weight(s[hh][2 * kg + 1][e + 1]);
                 E h0, h1, l0, l1;
-                split16x2(pa0, pa1, h0, h1, l0, l1);
+                if constexpr (kSplit) {
+                  split16x2(pa0, pa1, h0, h1, l0, l1);
+                  plo[hh][kg][e] = l0;
+                  plo[hh][kg][e + 1] = l1;
+                } else {
+                  round16x2_rtz(pa0, pa1, h0, h1);
+                }
                 phi[hh][kg][e] = h0;
                 phi[hh][kg][e + 1] = h1;
-                plo[hh][kg][e] = l0;
-                plo[hh][kg][e + 1] = l1;
-                split16x2(pb0, pb1, h0, h1, l0, l1);
+                if constexpr (kSplit) {
+                  split16x2(pb0, pb1, h0, h1, l0, l1);
+                  plo[hh][kg][4 + e] = l0;
+                  plo[hh][kg][5 + e] = l1;
+                } else {
+                  round16x2_rtz(pb0, pb1, h0, h1);
+                }
                 phi[hh][kg][4 + e] = h0;
                 phi[hh][kg][5 + e] = h1;
-                plo[hh][kg][4 + e] = l0;
-                plo[hh][kg][5 + e] = l1;
               }
             // Row sums: an all-ones A operand against P^T puts sum_k P[r][k] of the
             // tile's 32-key group in every entry of lane r's accumulator.
 #pragma unroll
             for (int kg = 0; kg < 2; ++kg) {
               lacc[hh] = M::mma(ones, phi[hh][kg], lacc[hh]);
-              lacc[hh] = M::mma(ones, plo[hh][kg], lacc[hh]);
+              if constexpr (kSplit) lacc[hh] = M::mma(ones, plo[hh][kg], lacc[hh]);
             }
           }
           // O^T += V^T P^T. Lane L reads tile row 32kg + 4g + L/4 (and +16), dims
@@ -410,7 +429,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
 #pragma unroll
               for (int hh = 0; hh < kHeadsPerWave; ++hh) {
                 o[hh][mt] = M::mma(a, phi[hh][kg], o[hh][mt]);
-                o[hh][mt] = M::mma(a, plo[hh][kg], o[hh][mt]);
+                if constexpr (kSplit) o[hh][mt] = M::mma(a, plo[hh][kg], o[hh][mt]);
               }
             }
           }

@@ -157,7 +157,8 @@ def test_config5_mixed_step_into_churned_pool(ie, O, dev, kv, impl):
 @pytest.mark.parametrize("kv", list(KVS))
 def test_mfma_forced(ie, O, dev, kv):
     """IMPL_MFMA runs the matrix-core prefill kernels for every KV type: 16-bit caches
-    in their own type with hi + lo operands, f32 caches on the f32 matrix instructions."""
+    in their own type (f16: q and P rounded once; bf16: hi + lo operands), f32 caches on
+    the f32 matrix instructions."""
     kvt = KVS[kv]
     rng = np.random.default_rng(41)
     tables, max_pages, num_pages = make_tables([333], rng)
