@@ -101,7 +101,15 @@ struct RowNorm {
   float eps;
 };
 
-template <bool GATE, int RT, int TT, int W, bool I8, bool NORM = false>
+// STAGED (the 8-wave, one-token-tile launches; cols % 32 == 0): the K blocks'
+// weight and activation tiles reach each wave's own LDS stages by DMA
+// (global_load_lds_dwordx4) in whole 64-byte row pieces, one block ahead, and
+// the MFMA operands are read back from there. A lane's direct loads of its
+// operands (row r, columns 8g..8g+7) put 16 rows into each quarter-wave, one
+// L1 access per lane; the L1 access rate then bounded these launches (probe,
+// down 896 x 4,864 at 64 tokens: 15.3 us direct, 8.5 us staged). The MFMA
+// operands and their order are the same, so the results are the same bits.
+template <bool GATE, int RT, int TT, int W, bool I8, bool NORM = false, bool STAGED = false>
 __global__ void __launch_bounds__(64 * W)
 matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const void* __restrict__ w,
                    const float* __restrict__ scale, const void* __restrict__ w2,
@@ -111,7 +119,8 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
   static_assert(NT <= 16, "at most 16 accumulator tiles (64 KB of LDS for the reduction)");
   __shared__ f32x4 red[W / 2][NT][64];
   __shared__ float red_ss[NORM ? W / 2 : 1][TT][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, r = lane & 15;
   const int row0 = blockIdx.x * 16 * RT, tok0 = blockIdx.y * 16 * TT;
   size_t wrow[RT];
@@ -130,6 +139,112 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
   float ss[TT];  // NORM: this lane's sum of x^2 of its token (row r of token tile j)
 #pragma unroll
   for (int j = 0; j < TT; ++j) ss[j] = 0.0f;
+  if constexpr (STAGED) {
+    static_assert(TT == 1 && W == 8, "staged: 8-wave, one-token-tile launches");
+    constexpr int kWTile = I8 ? 512 : 1024;               // 16 rows x 32 columns
+    constexpr int kStage = NA * RT * kWTile + 2048;        // + 16 tokens x 32 floats
+    constexpr int kPerStage = NA * RT + 2;                 // DMA instructions per stage
+    extern __shared__ __align__(16) unsigned char dyn[];
+    // [0, nbytes): the norm weight (NORM); then each wave's two stages.
+    const int nbytes = NORM ? cols * 4 : 0;
+    if constexpr (NORM) {
+      // Four loads in flight a thread (clamped indices), then the stores.
+      const float4* src = reinterpret_cast<const float4*>(norm.weight);
+      float4* dst = reinterpret_cast<float4*>(dyn);
+      const int n4 = cols / 4;
+      constexpr int S = 64 * W;
+      for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * S) {
+        const float4 v0 = src[min(i0, n4 - 1)], v1 = src[min(i0 + S, n4 - 1)];
+        const float4 v2 = src[min(i0 + 2 * S, n4 - 1)], v3 = src[min(i0 + 3 * S, n4 - 1)];
+        dst[i0] = v0;
+        if (i0 + S < n4) dst[i0 + S] = v1;
+        if (i0 + 2 * S < n4) dst[i0 + 2 * S] = v2;
+        if (i0 + 3 * S < n4) dst[i0 + 3 * S] = v3;
+      }
+      __syncthreads();
+    }
+    unsigned char* const stages = dyn + nbytes + wave * 2 * kStage;
+    const unsigned stages_lds = lds_address(stages);
+    // DMA sources. Weight tile: bf16, lane l takes row l/4, 16-byte piece
+    // (l%4) ^ (row/2 % 4); int8, lanes 0-31, row l/2, piece (l%2) ^ (row/4 % 2).
+    // Activation tile: lane l of DMA u takes token 8u + l/8, piece (l%8) ^ (l/8).
+    // LDS slot = lane, so each row's pieces land swizzled and the operand reads
+    // below spread over the banks.
+    const int wr = I8 ? (lane >> 1) : (lane >> 2);
+    const int wp = I8 ? ((lane & 1) ^ ((wr >> 2) & 1)) : ((lane & 3) ^ ((wr >> 1) & 3));
+    const char* wsrc[NA][RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const size_t off = (size_t(min(row0 + 16 * i + (wr & 15), rows - 1)) * cols + 8 * (I8 ? 2 : 1) * wp) *
+                         (I8 ? 1 : 2);
+      wsrc[0][i] = static_cast<const char*>(w) + off;
+      if constexpr (GATE) wsrc[NA - 1][i] = static_cast<const char*>(w2) + off;
+    }
+    const int xq = (lane & 7) ^ ((lane >> 3) & 7);
+    const float* xsrc0 = x + size_t(min(tok0 + (lane >> 3), T - 1)) * cols + 4 * xq;
+    const float* xsrc1 = x + size_t(min(tok0 + 8 + (lane >> 3), T - 1)) * cols + 4 * xq;
+    const int nblk = cols > 32 * wave ? (cols - 32 * wave + 32 * W - 1) / (32 * W) : 0;
+    auto issue = [&](const int slot, const int j) {
+      const int kb = min(32 * (wave + W * j), cols - 32);  // past the last block: any in-bounds one
+      const unsigned dst = stages_lds + slot * kStage;
+#pragma unroll
+      for (int n = 0; n < NA; ++n)
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          const char* src = wsrc[n][i] + size_t(kb) * (I8 ? 1 : 2);
+          if constexpr (I8) {
+            if (lane < 32) dma16(src, dst + (n * RT + i) * kWTile);
+          } else {
+            dma16(src, dst + (n * RT + i) * kWTile);
+          }
+        }
+      dma16(xsrc0 + kb, dst + NA * RT * kWTile);
+      dma16(xsrc1 + kb, dst + NA * RT * kWTile + 1024);
+    };
+    // Operand offsets in a stage (the inverse of the swizzles above).
+    const int aoff = I8 ? 16 * (2 * r + ((g >> 1) ^ ((r >> 2) & 1))) + 8 * (g & 1)
+                        : 16 * (4 * r + (g ^ ((r >> 1) & 3)));
+    const int boff0 = NA * RT * kWTile + 16 * (8 * r + ((2 * g) ^ (r & 7)));
+    const int boff1 = NA * RT * kWTile + 16 * (8 * r + ((2 * g + 1) ^ (r & 7)));
+    issue(0, 0);
+    for (int j = 0; j < nblk; ++j) {
+      issue((j + 1) & 1, j + 1);
+      wait_vmcnt<kPerStage>();  // block j's tiles have landed (block j + 1's may not)
+      const unsigned char* st = stages + (j & 1) * kStage;
+      float4 x0 = *reinterpret_cast<const float4*>(st + boff0);
+      float4 x1 = *reinterpret_cast<const float4*>(st + boff1);
+      if constexpr (NORM) {
+        const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss[0] = __builtin_fmaf(v[e], v[e], ss[0]);
+        const float* wn = reinterpret_cast<const float*>(dyn) + 32 * (wave + W * j) + 8 * g;
+        const float4 wn0 = *reinterpret_cast<const float4*>(wn);
+        const float4 wn1 = *reinterpret_cast<const float4*>(wn + 4);
+        x0 = make_float4(x0.x * wn0.x, x0.y * wn0.y, x0.z * wn0.z, x0.w * wn0.w);
+        x1 = make_float4(x1.x * wn1.x, x1.y * wn1.y, x1.z * wn1.z, x1.w * wn1.w);
+      }
+      bf16x8 bh, bm, bl;
+      split3(x0, x1, bh, bm, bl);
+#pragma unroll
+      for (int n = 0; n < NA; ++n)
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          bf16x8 a;
+          if constexpr (I8) {
+            const uint2 raw = *reinterpret_cast<const uint2*>(st + (n * RT + i) * kWTile + aoff);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const uint32_t word = e < 4 ? raw.x : raw.y;
+              a[e] = static_cast<bf16>(static_cast<float>(static_cast<int8_t>((word >> (8 * (e & 3))) & 0xFF)));
+            }
+          } else {
+            a = *reinterpret_cast<const bf16x8*>(st + (n * RT + i) * kWTile + aoff);
+          }
+          acc[n][i][0] = mma3(a, bh, bm, bl, acc[n][i][0]);
+        }
+    }
+    wait_vmcnt<0>();  // the extra block's DMA must land before the workgroup ends
+  } else
   for (int kb = 32 * wave; kb < cols; kb += 32 * W) {
     const int k = kb + 8 * g;
     const bool kin = k < cols;
@@ -304,6 +419,46 @@ int check_matrix(const ie_matrix& m, const char* who) {
   return IE_HIP_OK;
 }
 
+// The staged kernel's launch: dynamic LDS = the norm weight (NORM) + two stages
+// for each of the 8 waves. Returns false (nothing launched) when that exceeds
+// kStagedMaxLds; *rc is the launch status otherwise.
+constexpr int kStagedMaxLds = 128 * 1024;
+
+template <bool G, int R, bool I8, bool N>
+bool launch_staged_variant(const dim3 grid, hipStream_t stream, float* y, const float* x,
+                           const ie_matrix& w, const void* w2d, const float* s2, const float* bias,
+                           int T, int accumulate, RowSplit split, RowNorm norm, int* rc) {
+  constexpr int kStage = (G ? 2 : 1) * R * (I8 ? 512 : 1024) + 2048;
+  const size_t lds = (N ? size_t(w.cols) * 4 : 0) + size_t(2 * kMmWaves) * kStage;
+  if (lds > size_t(kStagedMaxLds)) return false;
+  const void* kernel = reinterpret_cast<const void*>(matmul_mfma_kernel<G, R, 1, kMmWaves, I8, N, true>);
+  if (lds > 64 * 1024) {  // above the default dynamic-LDS cap, within gfx950's 160 KB
+    static const hipError_t attr =
+        hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kStagedMaxLds);
+    if ((*rc = check_hip(attr, "hipFuncSetAttribute(matmul)"))) return true;
+  }
+  hipLaunchKernelGGL((matmul_mfma_kernel<G, R, 1, kMmWaves, I8, N, true>), grid, dim3(64 * kMmWaves),
+                     lds, stream, y, x, w.data, w.scale, w2d, s2, bias, T, w.rows, w.cols, accumulate,
+                     split, norm);
+  *rc = IE_HIP_OK;
+  return true;
+}
+
+template <bool G, int R>
+bool launch_staged_rt(bool i8, bool n, const dim3 grid, hipStream_t stream, float* y,
+                      const float* x, const ie_matrix& w, const void* w2d, const float* s2,
+                      const float* bias, int T, int accumulate, RowSplit split, RowNorm norm,
+                      int* rc) {
+#define IE_MM_STAGED(I, N_)                                                                    return launch_staged_variant<G, R, I, N_>(grid, stream, y, x, w, w2d, s2, bias, T, accumulate,                                             split, norm, rc)
+  if (i8) {
+    if (n) IE_MM_STAGED(true, true);
+    IE_MM_STAGED(true, false);
+  }
+  if (n) IE_MM_STAGED(false, true);
+  IE_MM_STAGED(false, false);
+#undef IE_MM_STAGED
+}
+
 int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const ie_matrix* w2,
                   const float* bias, int T, int accumulate, hipStream_t stream, const char* who,
                   RowSplit split = RowSplit{nullptr, nullptr, 0, 0},
@@ -351,6 +506,26 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   if (grid.y > 65535) return fail(IE_HIP_EINVAL, std::string(who) + ": too many tokens");
   const void* w2d = gate ? w2->data : nullptr;
   const float* s2 = gate ? w2->scale : nullptr;
+  // Every 8-wave launch whose K is whole 32-column blocks (and whose weights are
+  // 16-byte aligned, for the DMA) takes the staged kernel; the same operands in
+  // the same order, so the same results as the direct loads below.
+  if (!wide && w.cols % 32 == 0 &&
+      ((reinterpret_cast<uintptr_t>(w.data) | reinterpret_cast<uintptr_t>(w2d)) & 15) == 0) {
+    int rc = IE_HIP_OK;
+    const bool n = norm.weight != nullptr;
+    bool launched;
+    if (gate)
+      launched = RT == 2 ? launch_staged_rt<true, 2>(w.int8, n, grid, stream, y, x, w, w2d, s2, bias,
+                                                     T, accumulate, split, norm, &rc)
+                         : launch_staged_rt<true, 1>(w.int8, n, grid, stream, y, x, w, w2d, s2, bias,
+                                                     T, accumulate, split, norm, &rc);
+    else
+      launched = RT == 2 ? launch_staged_rt<false, 2>(w.int8, n, grid, stream, y, x, w, w2d, s2, bias,
+                                                      T, accumulate, split, norm, &rc)
+                         : launch_staged_rt<false, 1>(w.int8, n, grid, stream, y, x, w, w2d, s2, bias,
+                                                      T, accumulate, split, norm, &rc);
+    if (launched) return rc != IE_HIP_OK ? rc : check_launch(who);
+  }
   if (norm.weight) {
     // The folded rmsnorm exists for the 8-wave, one-token-tile launches (every
     // matrix below 16 row tiles per compute unit).
