@@ -498,7 +498,14 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   const int waves = wide ? 4 : kMmWaves;
   const int64_t tiles = int64_t((w.rows + 15) / 16) * ((T + 15) / 16);
   int RT = wide ? 4 : tiles >= 4 * int64_t(cus) ? 2 : 1;
-  if (gate) RT = std::min(RT, 2);  // two weight matrices: at most 2 row tiles
+  // The staged kernel (below) for every 8-wave launch whose K is whole 32-column
+  // blocks and whose weights are 16-byte aligned (for the DMA).
+  const bool staged = !wide && w.cols % 32 == 0 &&
+                      ((reinterpret_cast<uintptr_t>(w.data) |
+                        reinterpret_cast<uintptr_t>(w2 ? w2->data : nullptr)) & 15) == 0;
+  // Two weight matrices: at most 2 row tiles; staged, one (its LDS then fits two
+  // workgroups on a compute unit: config 6's gate/up, 1.657 -> 1.608 ms a step).
+  if (gate) RT = std::min(RT, staged ? 1 : 2);
   const int tok_tiles = (T + 15) / 16;  // kernels exist for 1, 2 and 4 token tiles
   const int TT = !wide ? 1 : tok_tiles > 2 ? 4 : tok_tiles;
   const dim3 grid((w.rows + 16 * RT - 1) / (16 * RT), (T + 16 * TT - 1) / (16 * TT));
@@ -506,11 +513,9 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   if (grid.y > 65535) return fail(IE_HIP_EINVAL, std::string(who) + ": too many tokens");
   const void* w2d = gate ? w2->data : nullptr;
   const float* s2 = gate ? w2->scale : nullptr;
-  // Every 8-wave launch whose K is whole 32-column blocks (and whose weights are
-  // 16-byte aligned, for the DMA) takes the staged kernel; the same operands in
-  // the same order, so the same results as the direct loads below.
-  if (!wide && w.cols % 32 == 0 &&
-      ((reinterpret_cast<uintptr_t>(w.data) | reinterpret_cast<uintptr_t>(w2d)) & 15) == 0) {
+  // The staged kernel: the same operands in the same order, so the same results
+  // as the direct loads below.
+  if (staged) {
     int rc = IE_HIP_OK;
     const bool n = norm.weight != nullptr;
     bool launched;
