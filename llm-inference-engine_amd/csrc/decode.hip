@@ -519,17 +519,20 @@ int ie_hip_attention_chunks(int context_tokens, int chunk_tokens) {
 }
 
 int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
-  if (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) {
-    // Matrix-core kernel (measured on MI355X): 128-position chunks. Where that
-    // gives two workgroups per compute unit one wave streams each chunk; on
-    // smaller grids the kernel gives each of a chunk's four page pairs its own
-    // wave (same result), so all are in flight at once, and the merge reads half
-    // the partials 64-position chunks would make.
-    return 128;
-  }
   const int cus = device_compute_units();
   const int64_t rows = std::max(T, 1);
   const int ctx = std::max(max_context, 1);
+  if (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) {
+    // Matrix-core kernel (measured on MI355X): 256-position chunks where rows x
+    // chunks at full context still reach 4 workgroups per compute unit (64 rows
+    // of 4,096: 19.6 against 21.0 us per call at 128; 512 positions 25.1 us),
+    // else 128 (one row of 32,768: 11.9 us per layer against 14.1 at 256; 48
+    // rows of 2,049: the decode part 14.8 against 16.3 us). Where the grid gives
+    // two workgroups per compute unit one wave streams each chunk; on smaller
+    // grids each of a chunk's page pairs gets its own wave (same result), so all
+    // are in flight at once.
+    return rows * ie_hip_attention_chunks(ctx, 256) >= 4 * int64_t(cus) ? 256 : 128;
+  }
   // float32 (matrix-core kernel, one page in flight per wave; measured on
   // MI355X): the largest chunk up to 256 positions that still gives two
   // workgroups per compute unit -- long chains of pages per wave where the grid
