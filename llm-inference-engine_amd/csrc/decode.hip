@@ -523,21 +523,22 @@ int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
   const int64_t rows = std::max(T, 1);
   const int ctx = std::max(max_context, 1);
   if (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) {
-    // Matrix-core kernel (measured on MI355X): 256-position chunks where rows x
+    // Matrix-core kernel (measured on MI355X): 192-position chunks where rows x
     // chunks at full context still reach 4 workgroups per compute unit (64 rows
-    // of 4,096: 19.6 against 21.0 us per call at 128; 512 positions 25.1 us),
+    // of 4,096: 18.5 us per call against 19.5 at 256, 21.0 at 128, 25.1 at 512),
     // else 128 (one row of 32,768: 11.9 us per layer against 14.1 at 256; 48
-    // rows of 2,049: the decode part 14.8 against 16.3 us). Where the grid gives
-    // two workgroups per compute unit one wave streams each chunk; on smaller
-    // grids each of a chunk's page pairs gets its own wave (same result), so all
-    // are in flight at once.
-    return rows * ie_hip_attention_chunks(ctx, 256) >= 4 * int64_t(cus) ? 256 : 128;
+    // rows of 2,049: the decode part 14.6 against 16.4 us at 192). Where the
+    // grid gives two workgroups per compute unit one wave streams each chunk; on
+    // smaller grids each of a chunk's page pairs gets its own wave (same
+    // result), so all are in flight at once.
+    return rows * ie_hip_attention_chunks(ctx, 192) >= 4 * int64_t(cus) ? 192 : 128;
   }
   // float32 (matrix-core kernel, one page in flight per wave; measured on
-  // MI355X): the largest chunk up to 256 positions that still gives two
+  // MI355X): the largest chunk up to 192 positions that still gives two
   // workgroups per compute unit -- long chains of pages per wave where the grid
-  // is large, short ones where few rows must fill the device.
-  for (int ct : {256, 128, 64})
+  // is large, short ones where few rows must fill the device (64 rows of 4,096:
+  // 33.6 us per call at 192, 35.6 at 256, 40.5 at 128).
+  for (int ct : {192, 128, 64})
     if (rows * ie_hip_attention_chunks(ctx, ct) >= 2 * cus) return ct;
   return 32;
 }

@@ -95,19 +95,19 @@ def test_chunk_helpers(ie):
     assert ie.attention_chunks(4096, 512) == 8
     assert ie.attention_chunks(4097, 512) == 9
     assert ie.attention_chunks(1, 16) == 1
-    # 16-bit caches (matrix-core kernel): 256-token chunks where rows x chunks at full
+    # 16-bit caches (matrix-core kernel): 192-token chunks where rows x chunks at full
     # context reach 4 workgroups per compute unit, else 128 (small grids take one wave
-    # per page pair); float32: the largest chunk up to 256 that still gives two
+    # per page pair); float32: the largest chunk up to 192 that still gives two
     # workgroups per compute unit, else 32. No GPU here: the helper assumes MI355X's 256
     # compute units.
-    assert ie.attention_chunk_tokens(64, 4096, ie.KV_F16) == 256   # 64 x 16 = 1,024
-    assert ie.attention_chunk_tokens(64, 4096, ie.KV_BF16) == 256
-    assert ie.attention_chunk_tokens(64, 3840, ie.KV_F16) == 128   # 64 x 15 < 1,024
-    assert ie.attention_chunk_tokens(48, 2049, ie.KV_F16) == 128   # 48 x 9
-    assert ie.attention_chunk_tokens(1, 32768, ie.KV_F16) == 128
+    assert ie.attention_chunk_tokens(64, 4096, ie.KV_F16) == 192   # 64 x 22 = 1,408
+    assert ie.attention_chunk_tokens(64, 4096, ie.KV_BF16) == 192
+    assert ie.attention_chunk_tokens(64, 2880, ie.KV_F16) == 128   # 64 x 15 < 1,024
+    assert ie.attention_chunk_tokens(48, 2049, ie.KV_F16) == 128   # 48 x 11
+    assert ie.attention_chunk_tokens(1, 32768, ie.KV_F16) == 128   # 1 x 171
     assert ie.attention_chunk_tokens(1, 8192, ie.KV_BF16) == 128
-    assert ie.attention_chunk_tokens(8, 131072, ie.KV_BF16) == 256  # 8 x 512
-    assert ie.attention_chunk_tokens(64, 4096, ie.KV_F32) == 256
+    assert ie.attention_chunk_tokens(8, 131072, ie.KV_BF16) == 192  # 8 x 683
+    assert ie.attention_chunk_tokens(64, 4096, ie.KV_F32) == 192
     assert ie.attention_chunk_tokens(1, 32768, ie.KV_F32) == 64
     assert ie.attention_chunk_tokens(1, 1, ie.KV_F32) == 32
     n = ie.lib().ie_hip_attention_workspace_bytes(64, 14, 64, 8)

@@ -377,7 +377,7 @@ def test_out_of_pool_pages_are_skipped(ie, O, dev, kv, impl):
 
 BATCH_SHAPES = [
     # rows, context length range [lo, hi), chunk tokens (None: the library's choice)
-    (64, (128, 4097), None),  # BASELINE config 3's shape (the library's 256-token chunks)
+    (64, (128, 4097), None),  # BASELINE config 3's shape (the library's 192-token chunks)
     (64, (1, 300), 64),
     (200, (1, 2000), 128),
     (256, (1, 700), 64),

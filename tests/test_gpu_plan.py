@@ -77,10 +77,10 @@ def test_planned_equals_unplanned(ie, O, dev, kv, case):
         f"planned differs ({T} rows, chunk {ct}, {nc} chunks)"
 
 
-@pytest.mark.parametrize("ct", [128, 256])
+@pytest.mark.parametrize("ct", [128, 192, 256])
 def test_config3_planned_full_size(ie, O, dev, ct):
     """64 rows, L ~ U[128, 4096], 65,536-page f16 pools, shuffled
-    tables; 256-token chunks (the library's choice for this grid) and 128."""
+    tables; 192-token chunks (the library's choice for this grid), 128 and 256."""
     rng = np.random.default_rng(20263)
     T, num_pages = 64, 65536
     lens = rng.integers(128, 4097, T)
