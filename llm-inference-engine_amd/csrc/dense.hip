@@ -491,8 +491,9 @@ int launch_matmul(bool gate, float* y, const float* x, const ie_matrix& w, const
   // Otherwise 8 waves, and the tiles per workgroup (which do not change the
   // arithmetic) follow the count of 16 x 16 output tiles, measured at 64
   // tokens: below 4 per compute unit (q/k/v/o and down at 896 rows) one tile
-  // per workgroup keeps every unit busy; from 4 per unit (gate/up's 4,864
-  // rows) two row tiles share each activation fragment.
+  // per workgroup keeps every unit busy; from 4 per unit two row tiles share
+  // each activation fragment, except for gate/up in the staged kernel (one row
+  // tile, below).
   const int cus = device_compute_units();
   const bool wide = (w.rows + 15) / 16 >= 16 * cus;
   const int waves = wide ? 4 : kMmWaves;
