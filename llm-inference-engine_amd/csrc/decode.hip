@@ -534,11 +534,13 @@ int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
     return rows * ie_hip_attention_chunks(ctx, 192) >= 4 * int64_t(cus) ? 192 : 128;
   }
   // float32 (matrix-core kernel, one page in flight per wave; measured on
-  // MI355X): the largest chunk up to 192 positions that still gives two
-  // workgroups per compute unit -- long chains of pages per wave where the grid
-  // is large, short ones where few rows must fill the device (64 rows of 4,096:
-  // 33.6 us per call at 192, 35.6 at 256, 40.5 at 128).
-  for (int ct : {192, 128, 64})
+  // MI355X): 192 positions where that gives 4 workgroups per compute unit (64
+  // rows of 4,096: 33.6 us per call at 192, 35.6 at 256, 40.5 at 128), else the
+  // largest of 128 and 64 that still gives two (48 rows of 2,049: 25.0 us at 128
+  // against 29.5 at 192; one row of 32,768: 64) -- long chains of pages per wave
+  // where the grid is large, short ones where few rows must fill the device.
+  if (rows * ie_hip_attention_chunks(ctx, 192) >= 4 * int64_t(cus)) return 192;
+  for (int ct : {128, 64})
     if (rows * ie_hip_attention_chunks(ctx, ct) >= 2 * cus) return ct;
   return 32;
 }

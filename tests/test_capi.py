@@ -97,8 +97,8 @@ def test_chunk_helpers(ie):
     assert ie.attention_chunks(1, 16) == 1
     # 16-bit caches (matrix-core kernel): 192-token chunks where rows x chunks at full
     # context reach 4 workgroups per compute unit, else 128 (small grids take one wave
-    # per page pair); float32: the largest chunk up to 192 that still gives two
-    # workgroups per compute unit, else 32. No GPU here: the helper assumes MI355X's 256
+    # per page pair); float32: 192 where that reaches 4 workgroups per compute unit,
+    # else the largest of 128 and 64 that still gives two, else 32. No GPU here: the helper assumes MI355X's 256
     # compute units.
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_F16) == 192   # 64 x 22 = 1,408
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_BF16) == 192
@@ -108,6 +108,7 @@ def test_chunk_helpers(ie):
     assert ie.attention_chunk_tokens(1, 8192, ie.KV_BF16) == 128
     assert ie.attention_chunk_tokens(8, 131072, ie.KV_BF16) == 192  # 8 x 683
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_F32) == 192
+    assert ie.attention_chunk_tokens(48, 2049, ie.KV_F32) == 128   # 48 x 11 < 1,024
     assert ie.attention_chunk_tokens(1, 32768, ie.KV_F32) == 64
     assert ie.attention_chunk_tokens(1, 1, ie.KV_F32) == 32
     n = ie.lib().ie_hip_attention_workspace_bytes(64, 14, 64, 8)
