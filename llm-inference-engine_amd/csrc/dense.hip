@@ -147,22 +147,6 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
     extern __shared__ __align__(16) unsigned char dyn[];
     // [0, nbytes): the norm weight (NORM); then each wave's two stages.
     const int nbytes = NORM ? cols * 4 : 0;
-    if constexpr (NORM) {
-      // Four loads in flight a thread (clamped indices), then the stores.
-      const float4* src = reinterpret_cast<const float4*>(norm.weight);
-      float4* dst = reinterpret_cast<float4*>(dyn);
-      const int n4 = cols / 4;
-      constexpr int S = 64 * W;
-      for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * S) {
-        const float4 v0 = src[min(i0, n4 - 1)], v1 = src[min(i0 + S, n4 - 1)];
-        const float4 v2 = src[min(i0 + 2 * S, n4 - 1)], v3 = src[min(i0 + 3 * S, n4 - 1)];
-        dst[i0] = v0;
-        if (i0 + S < n4) dst[i0 + S] = v1;
-        if (i0 + 2 * S < n4) dst[i0 + 2 * S] = v2;
-        if (i0 + 3 * S < n4) dst[i0 + 3 * S] = v3;
-      }
-      __syncthreads();
-    }
     unsigned char* const stages = dyn + nbytes + wave * 2 * kStage;
     const unsigned stages_lds = lds_address(stages);
     // DMA sources. Weight tile: bf16, lane l takes row l/4, 16-byte piece
@@ -185,7 +169,7 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
     const float* xsrc1 = x + size_t(min(tok0 + 8 + (lane >> 3), T - 1)) * cols + 4 * xq;
     const int nblk = cols > 32 * wave ? (cols - 32 * wave + 32 * W - 1) / (32 * W) : 0;
     auto issue = [&](const int slot, const int j) {
-      const int kb = min(32 * (wave + W * j), cols - 32);  // past the last block: any in-bounds one
+      const int kb = min(32 * (wave + W * j), cols - 32);  // j < nblk: always in bounds
       const unsigned dst = stages_lds + slot * kStage;
 #pragma unroll
       for (int n = 0; n < NA; ++n)
@@ -206,10 +190,26 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
                         : 16 * (4 * r + (g ^ ((r >> 1) & 3)));
     const int boff0 = NA * RT * kWTile + 16 * (8 * r + ((2 * g) ^ (r & 7)));
     const int boff1 = NA * RT * kWTile + 16 * (8 * r + ((2 * g + 1) ^ (r & 7)));
-    issue(0, 0);
+    // Blocks 0 and 1 go out first. NORM: then the norm weight, also by DMA (so
+    // that every wait here is on this wave's own count of DMAs), and the whole
+    // workgroup waits for it: its round trip overlaps the blocks' instead of
+    // preceding them.
+    if (nblk > 0) issue(0, 0);
+    if (nblk > 1) issue(1, 1);
+    if constexpr (NORM) {
+      const int n4 = cols / 4;  // 16-byte pieces; lane l of a DMA lands at base + 16 l
+      const unsigned norm_lds = lds_address(dyn);
+      for (int i0 = 64 * wave; i0 < n4; i0 += 64 * W)
+        if (i0 + lane < n4) dma16(norm.weight + 4 * (i0 + lane), norm_lds + 16 * i0);
+      wait_vmcnt<0>();
+      __syncthreads();
+    }
     for (int j = 0; j < nblk; ++j) {
-      issue((j + 1) & 1, j + 1);
-      wait_vmcnt<kPerStage>();  // block j's tiles have landed (block j + 1's may not)
+      // Block j's tiles have landed (block j + 1's, when there is one, may not).
+      if (j + 1 < nblk)
+        wait_vmcnt<kPerStage>();
+      else
+        wait_vmcnt<0>();
       const unsigned char* st = stages + (j & 1) * kStage;
       float4 x0 = *reinterpret_cast<const float4*>(st + boff0);
       float4 x1 = *reinterpret_cast<const float4*>(st + boff1);
@@ -242,8 +242,13 @@ matmul_mfma_kernel(float* __restrict__ y, const float* __restrict__ x, const voi
           }
           acc[n][i][0] = mma3(a, bh, bm, bl, acc[n][i][0]);
         }
+      // Block j + 2 into the stage just read, once those LDS reads are done
+      // (s_waitcnt lgkmcnt(0), the other counters at their no-wait maxima).
+      if (j + 2 < nblk) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        issue(j & 1, j + 2);
+      }
     }
-    wait_vmcnt<0>();  // the extra block's DMA must land before the workgroup ends
   } else
   for (int kb = 32 * wave; kb < cols; kb += 32 * W) {
     const int k = kb + 8 * g;
