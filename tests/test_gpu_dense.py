@@ -194,6 +194,41 @@ def test_rmsnorm_gate_up_silu(ie, dev, int8, T):
     assert rel_err(out.cpu().numpy(), want) <= REL
 
 
+@pytest.mark.parametrize("int8", [False, True])
+@pytest.mark.parametrize("cols", [32, 96, 2080, 4864])
+def test_rmsnorm_folds_widths(ie, dev, int8, cols):
+    """Both folds at hidden widths other than 896: the norm weight reaches LDS in
+    16-byte pieces, 64 to a wave and 512 to a pass of the 8 waves, so 32 and 96 leave
+    most lanes idle, 2,080 (520 pieces) takes a second pass and 4,864 three."""
+    rng = np.random.default_rng(60 + cols)
+    T, rows = 17, 96
+    x = rng.standard_normal((T, cols), dtype=np.float32) * np.float32(4.0)
+    wn = rng.standard_normal(cols, dtype=np.float32)
+    wg32 = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+    wu32 = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+    mg, kg, (wg, fmt, sg) = dev_weights(ie, dev, wg32, int8)
+    mu, ku, (wu, _, su) = dev_weights(ie, dev, wu32, int8)
+    dx, dwn = torch.from_numpy(x).to(dev), torch.from_numpy(wn).to(dev)
+    out = torch.full((T, rows), float("nan"), device=dev)
+    ie.rmsnorm_gate_up_silu(out, dx, dwn, EPS, mg, mu)
+    QD, KVD = 64, 16
+    b = rng.standard_normal(QD + 2 * KVD, dtype=np.float32)
+    wq32 = rng.standard_normal((QD + 2 * KVD, cols), dtype=np.float32) * np.float32(0.05)
+    mq, kq, (wq, fmtq, sq) = dev_weights(ie, dev, wq32, int8)
+    q = torch.full((T, QD), float("nan"), device=dev)
+    k = torch.full((T, KVD), float("nan"), device=dev)
+    v = torch.full((T, KVD), float("nan"), device=dev)
+    ie.rmsnorm_qkv_proj(q, k, v, dx, dwn, EPS, mq, torch.from_numpy(b).to(dev))
+    torch.cuda.synchronize()
+    xn = O.rmsnorm(x, wn, EPS)
+    want = O.silu_mul(O.matmul(xn, wg, fmt, sg), O.matmul(xn, wu, fmt, su))
+    assert rel_err(out.cpu().numpy(), want) <= REL
+    wq_ = O.matmul(xn, wq, fmtq, sq, b)
+    assert rel_err(q.cpu().numpy(), wq_[:, :QD]) <= REL
+    assert rel_err(k.cpu().numpy(), wq_[:, QD:QD + KVD]) <= REL
+    assert rel_err(v.cpu().numpy(), wq_[:, QD + KVD:]) <= REL
+
+
 def test_rmsnorm_folds_batch_invariant(ie, dev):
     """A row's output is the same bits in a batch of 64 as alone (the sum of squares is
     reduced in an order fixed by the matrix shape)."""
