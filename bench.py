@@ -755,6 +755,7 @@ def _probe_lib():
     lib.ie_probe_read_form.argtypes = [vp, ctypes.c_size_t, i, i, vp, vp]
     lib.ie_probe_pages.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, vp, vp]
     lib.ie_probe_pages_form.argtypes = [vp, vp, vp, vp, vp, vp, i, i, i, i, i, vp, vp]
+    lib.ie_probe_pages_ring.argtypes = [vp, vp, vp, i, i, i, vp, vp]
     return lib
 
 
@@ -830,6 +831,39 @@ def hbm_probes(args, torch, stream, k_pools, v_pools, d_tab, lens, max_pages, ct
     out["page_walk_us"] = round(ms * 1e3, 3)
     out["page_walk_form"] = best[1]
     out["page_walk_bytes"] = walk_bytes
+
+    # The same pages as one flat list, walked by persistent one-wave workgroups with
+    # `ring` pages (K + V) in flight per wave: a shape of its own, not the kernel's.
+    flat = []
+    tab_h = d_tab.cpu().numpy()
+    for r, L in enumerate(lens):
+        flat.extend(int(x) for x in tab_h[r, :(int(L) + PAGE - 1) // PAGE])
+    d_flat = torch.tensor(flat, dtype=torch.int32, device=dev)
+    best = None
+    sweep = {}
+    if page_bytes == 4096:
+        for ring, per_cu in ((1, 16), (2, 8), (2, 10), (4, 4), (4, 5), (8, 2), (2, 4), (4, 2)):
+            waves = per_cu * cus
+            if len(flat) > 64 * waves:
+                continue
+
+            def ring_walk(i, ring=ring, waves=waves):
+                l = i % len(k_pools)
+                rc = lib.ie_probe_pages_ring(k_pools[l].data_ptr(), v_pools[l].data_ptr(),
+                                             d_flat.data_ptr(), len(flat), waves, ring,
+                                             sink.data_ptr(), sp())
+                assert rc == 0
+
+            ms = time_steps(torch, ring_walk, max(args.steps, 40), 5, stream)
+            sweep[f"r{ring}x{per_cu}"] = round(ms * 1e3, 3)
+            if best is None or ms < best[0]:
+                best = (ms, ring, per_cu)
+    if best is not None:
+        ms = best[0]
+        out["page_ring_gbs"] = round(walk_bytes / (ms * 1e-3) / 1e9, 1)
+        out["page_ring_us"] = round(ms * 1e3, 3)
+        out["page_ring_shape"] = {"pages_in_flight_per_wave": best[1], "waves_per_cu": best[2]}
+        out["page_ring_sweep_us"] = sweep
     out["ceiling_gbs"] = out["read_70MB_gbs"]
     return out
 

@@ -190,12 +190,21 @@ decode_partial_mfma(float* __restrict__ out, float* __restrict__ part_o,
     const int32_t* item = plan + kPlanHeader + size_t(blockIdx.x) * plan_stride(chunk_tokens);
     const int pg = wt0 / IE_HIP_PAGE_SIZE + lane;
     pid_plan = pg < chunk_tokens / IE_HIP_PAGE_SIZE ? item[4 + pg] : -1;
-    const int items = __builtin_amdgcn_readfirstlane(plan[0]);
+    const int4 head = *reinterpret_cast<const int4*>(plan);  // [items, chunk, chunks, rows]
+    const int items = __builtin_amdgcn_readfirstlane(head.x);
     t = __builtin_amdgcn_readfirstlane(item[0]);
     c = __builtin_amdgcn_readfirstlane(item[1]);
     p = __builtin_amdgcn_readfirstlane(item[2]);
     seq = __builtin_amdgcn_readfirstlane(item[3]);
     if (int(blockIdx.x) >= items) return;  // past the plan's last item
+    // A plan built for another launch (another chunk size, chunk count or row
+    // count) would address other slots: such a launch writes nothing. So does
+    // an item naming a row or chunk outside this launch's.
+    if (__builtin_amdgcn_readfirstlane(head.y) != chunk_tokens ||
+        __builtin_amdgcn_readfirstlane(head.z) != num_chunks ||
+        __builtin_amdgcn_readfirstlane(head.w) != T || t < 0 || t >= T || c < 0 ||
+        c >= num_chunks || p < c * chunk_tokens)
+      return;
   } else if (!locate_chunk(blockIdx.x, T, row_pos, row_seq, num_chunks, chunk_tokens, lane, t, c,
                            p, seq)) {
     return;  // past the batch's last chunk: the whole workgroup leaves

@@ -193,12 +193,15 @@ __device__ __forceinline__ void split16x2<__bf16>(float x0, float x1, __bf16& h0
   split16(x1, h1, l1);
 }
 
-// Two f32 values as one packed f16 pair rounded toward zero (v_cvt_pkrtz_f16_f32):
-// |x - h| < 2^-10 |x| for normal results.
-__device__ __forceinline__ void round16x2_rtz(float x0, float x1, _Float16& h0, _Float16& h1) {
-  const unsigned hb = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-  h0 = __builtin_bit_cast(_Float16, static_cast<unsigned short>(hb));
-  h1 = __builtin_bit_cast(_Float16, static_cast<unsigned short>(hb >> 16));
+// Two f32 values as one packed f16 pair rounded to nearest even
+// (v_cvt_pk_f16_f32 on gfx950): |x - h| <= 2^-11 |x| for normal results, the
+// rounding of __floats2half2_rn that the reference's tensor-core prefill
+// applies to its weights (src/cuda/kernels.cu:741).
+__device__ __forceinline__ void round16x2(float x0, float x1, _Float16& h0, _Float16& h1) {
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  const half2_t h = {static_cast<_Float16>(x0), static_cast<_Float16>(x1)};
+  h0 = h.x;
+  h1 = h.y;
 }
 
 // 2^x for the softmax weights: the bare v_exp_f32 (x <= 0 here; results below

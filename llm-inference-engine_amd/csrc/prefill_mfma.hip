@@ -18,12 +18,12 @@
 // reductions over the 4 lane groups.
 //
 // Precision: K and V enter exactly. With an f16 cache, q (pre-scaled by
-// log2(e)/8, rounded to nearest) and P (weights <= 2^kLazyMax, rounded toward
-// zero) enter as single f16 values -- the operand rounding of the reference's
-// tensor-core kernel (src/cuda/kernels.cu:673-674,741), here with the row sums
-// taken from the same rounded P on the matrix cores, so the output is a weighted
-// mean with weights off by < 2^-10 relative (errors ~6e-4 at 4,000 keys against
-// the 2e-3 absolute bound). bf16 keeps 8 mantissa bits, too few for that bound:
+// log2(e)/8) and P (weights <= 2^kLazyMax) enter as single f16 values rounded
+// to nearest -- the operand rounding of the reference's tensor-core kernel
+// (src/cuda/kernels.cu:673-674,741), here with the row sums taken from the same
+// rounded P on the matrix cores, so the output is a weighted mean with weights
+// off by <= 2^-11 relative (errors ~6e-4 at 4,000 keys against the 2e-3
+// absolute bound). bf16 keeps 8 mantissa bits, too few for that bound:
 // with a bf16 cache q and P are split into hi + lo halves and each product is
 // done twice (float32-level scores and weights, errors ~1e-6).
 //
@@ -390,7 +390,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
                   plo[hh][kg][e] = l0;
                   plo[hh][kg][e + 1] = l1;
                 } else {
-                  round16x2_rtz(pa0, pa1, h0, h1);
+                  round16x2(pa0, pa1, h0, h1);
                 }
                 phi[hh][kg][e] = h0;
                 phi[hh][kg][e + 1] = h1;
@@ -399,7 +399,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
                   plo[hh][kg][4 + e] = l0;
                   plo[hh][kg][5 + e] = l1;
                 } else {
-                  round16x2_rtz(pb0, pb1, h0, h1);
+                  round16x2(pb0, pb1, h0, h1);
                 }
                 phi[hh][kg][4 + e] = h0;
                 phi[hh][kg][5 + e] = h1;

@@ -166,6 +166,51 @@ probe_pages_dma_kernel(const unsigned char* __restrict__ k_pool,
   if (acc == 0x9E3779B9u) sink[w] = acc;
 }
 
+// A walk of random 4 KB pages that owes nothing to the decode kernel's shape:
+// persistent one-wave workgroups over a flat list of page ids (each entry = the
+// K page and the V page of that id, 8 KB), every wave a contiguous, balanced
+// range of the list, with R pages in flight per wave in an LDS ring of R
+// stages (non-temporal LDS DMA, 8 instructions of 1 KB per page). The wave
+// waits for the oldest page only (vmcnt counts the 8 x (R-1) instructions
+// issued after it), folds a word of it and refills its stage. A wave's range
+// is at most 64 pages (its ids are loaded once, one per lane).
+template <int R>
+__global__ void __launch_bounds__(64)
+probe_ring_kernel(const unsigned char* __restrict__ k_pool, const unsigned char* __restrict__ v_pool,
+                  const int32_t* __restrict__ pages, int n, uint32_t* __restrict__ sink) {
+  extern __shared__ __align__(16) unsigned char ring[];  // [R][2 pools][4096]
+  const int lane = threadIdx.x;
+  const int64_t waves = gridDim.x;
+  const int begin = int(int64_t(n) * blockIdx.x / waves);
+  const int cnt = int(int64_t(n) * (blockIdx.x + 1) / waves) - begin;
+  const int id_lane = lane < cnt ? pages[begin + lane] : 0;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const unsigned base = lds_base(ring);
+  auto issue = [&](const int u) {
+    const size_t off = size_t(__builtin_amdgcn_readlane(id_lane, u)) * 4096 + lane * 16;
+    const unsigned st = base + (u % R) * 8192;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_1k<true>(k_pool + off + i * 1024, st + i * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_1k<true>(v_pool + off + i * 1024, st + 4096 + i * 1024);
+  };
+  for (int u = 0; u < R && u < cnt; ++u) issue(u);
+  uint32_t acc = 0;
+  for (int u = 0; u < cnt; ++u) {
+    if (u + R - 1 < cnt) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (R - 1)) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    const unsigned char* st = ring + (u % R) * 8192;
+    acc ^= fold(*reinterpret_cast<const uint4*>(st + lane * 16)) ^
+           fold(*reinterpret_cast<const uint4*>(st + 4096 + lane * 16));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the stage is read before it is refilled
+    if (u + R < cnt) issue(u + R);
+  }
+  if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
 template <bool NT>
 int probe_pages(const void* k_pool, const void* v_pool, const int32_t* tables,
                        const int32_t* work_row, const int32_t* work_chunk, const int32_t* row_len,
@@ -243,6 +288,49 @@ int ie_probe_pages_form(const void* k_pool, const void* v_pool, const int32_t* t
                      static_cast<const unsigned char*>(k_pool),
                      static_cast<const unsigned char*>(v_pool), tables, work_row, work_chunk,
                      row_len, max_pages, chunk_tokens, page_bytes, sink);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// The persistent ring walk: `waves` one-wave workgroups over the flat list of
+// n page ids (each the K page and the V page of that id, 4 KB each), `ring`
+// pages in flight per wave (1, 2, 4 or 8; ring x 8 KB of LDS per wave). Every
+// wave's range must fit 64 pages: n <= 64 x waves.
+int ie_probe_pages_ring(const void* k_pool, const void* v_pool, const int32_t* pages, int n,
+                        int waves, int ring, uint32_t* sink, hipStream_t stream) {
+  if (!k_pool || !v_pool || !pages || !sink || n <= 0 || waves <= 0 ||
+      int64_t(n) > 64 * int64_t(waves))
+    return 1;
+  const dim3 g(waves), b(64);
+  const size_t lds = size_t(ring) * 8192;
+  switch (ring) {
+    case 1:
+      hipLaunchKernelGGL(probe_ring_kernel<1>, g, b, lds, stream,
+                         static_cast<const unsigned char*>(k_pool),
+                         static_cast<const unsigned char*>(v_pool), pages, n, sink);
+      break;
+    case 2:
+      hipLaunchKernelGGL(probe_ring_kernel<2>, g, b, lds, stream,
+                         static_cast<const unsigned char*>(k_pool),
+                         static_cast<const unsigned char*>(v_pool), pages, n, sink);
+      break;
+    case 4:
+      hipLaunchKernelGGL(probe_ring_kernel<4>, g, b, lds, stream,
+                         static_cast<const unsigned char*>(k_pool),
+                         static_cast<const unsigned char*>(v_pool), pages, n, sink);
+      break;
+    case 8: {
+      static const hipError_t attr = hipFuncSetAttribute(
+          reinterpret_cast<const void*>(probe_ring_kernel<8>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+      if (attr != hipSuccess) return 2;
+      hipLaunchKernelGGL(probe_ring_kernel<8>, g, b, lds, stream,
+                         static_cast<const unsigned char*>(k_pool),
+                         static_cast<const unsigned char*>(v_pool), pages, n, sink);
+      break;
+    }
+    default:
+      return 1;
+  }
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

@@ -153,3 +153,93 @@ def test_planned_refuses_a_short_plan(ie, dev):
     ws = ie.attention_workspace(T, NH, HD, nc)
     with pytest.raises(ie.IeHipError, match="plan holds"):
         ie.attention_planned(z, z, pool, pool, idx, idx, tab, 1, nc, ct, ws, small, NH, NKV, HD)
+
+
+def test_config4_fused_planned_full_size(ie, O, dev):
+    """BASELINE config 4's benched call at full size: one row at position 32,767, bf16
+    pages in a shuffled table, the library's chunk size for that grid,
+    rope_cache_attention_planned. Pages bit-exact against the oracle's RoPE + append,
+    attention within 2e-3 of the oracle over all 32,768 positions, and the same bits as
+    ie_hip_rope_and_cache followed by ie_hip_attention."""
+    kvt = KVS["bf16"]
+    rng = np.random.default_rng(20264)
+    L = 32768
+    tables, max_pages, num_pages = make_tables([L], rng, extra_pages=64)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    pos, seq = np.array([L - 1], np.int32), np.zeros(1, np.int32)
+    q, k, v = normal(rng, (1, QD)), normal(rng, (1, KVD)), normal(rng, (1, KVD))
+    ct = ie.attention_chunk_tokens(1, L, kvt)
+    nc = ie.attention_chunks(L, ct)
+    table = ie.rope_table(L, HD, 1e6).to(dev)
+    plan = torch.from_numpy(ie.attention_plan(pos, seq, tables, nc, ct)).to(dev)
+    d_pos, d_seq, d_tab = to_dev(pos, dev), to_dev(seq, dev), to_dev(tables, dev)
+    dk, dv = to_dev(k, dev), to_dev(v, dev)
+    ws = ie.attention_workspace(1, NH, HD, nc)
+
+    fkp, fvp = to_dev(kp, dev, kvt), to_dev(vp, dev, kvt)
+    fout = torch.full((1, QD), float("nan"), device=dev)
+    ie.rope_cache_attention_planned(fout, to_dev(q, dev), dk, dv, fkp, fvp, table, d_pos, d_seq,
+                                    d_tab, int(max_pages), nc, ct, ws, plan, NH, NKV, HD)
+    tkp, tvp = to_dev(kp, dev, kvt), to_dev(vp, dev, kvt)
+    tq = to_dev(q, dev)
+    tout = torch.full((1, QD), float("nan"), device=dev)
+    ws2 = ie.attention_workspace(1, NH, HD, nc)
+    ie.rope_and_cache(tq, dk, dv, tkp, tvp, table, d_pos, d_seq, d_tab, int(max_pages), NH, NKV,
+                      HD)
+    ie.attention(tout, tq, tkp, tvp, d_pos, d_seq, d_tab, int(max_pages), nc, ct, ws2, NH, NKV,
+                 HD)
+    torch.cuda.synchronize()
+
+    q_ref, kp_ref, vp_ref = O.rope_append_paged(q, k, v, kp, vp, kvt, pos, seq, tables,
+                                                int(max_pages), NH, NKV, HD, 1e6)
+    assert np.array_equal(from_dev(fkp), kp_ref) and np.array_equal(from_dev(fvp), vp_ref)
+    want = O.paged_attention(q_ref, kp_ref, vp_ref, kvt, pos, seq, tables, int(max_pages), NH,
+                             NKV, HD, threads=8)
+    got = from_dev(fout)
+    assert np.all(np.isfinite(got))
+    err = float(np.abs(got - want).max())
+    assert err <= 2e-3, f"config 4: abs err {err:.3e} (chunk {ct}, {nc} chunks)"
+    assert np.array_equal(got.view(np.uint32), from_dev(tout).view(np.uint32))
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_mismatched_plan_writes_nothing(ie, O, dev, fused):
+    """A plan built for another launch -- another chunk size, or another row count --
+    passes the host's capacity check but would address other slots: the kernel
+    compares the plan's header with its own arguments and writes nothing, neither
+    partials, nor a single-chunk row's output, nor (fused) the appended rows. The
+    merge kernel still runs over the untouched workspace, inside its bounds; the
+    guard words past `out` and the workspace stay as they were."""
+    kvt = KVS["f16"]
+    rng = np.random.default_rng(1500 + fused)
+    lens = np.array([100, 700, 1500])
+    T = len(lens)
+    tables, max_pages, num_pages = make_tables(lens, rng, extra_pages=3)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    pos, seq = (lens - 1).astype(np.int32), np.arange(T, dtype=np.int32)
+    ct, nc = 256, ie.attention_chunks(1500, 256)
+    plans = [ie.attention_plan(pos, seq, tables, ie.attention_chunks(1500, 128), 128),
+             ie.attention_plan(pos[:2], seq[:2], tables, 2 * nc, ct)]
+    q, k, v = normal(rng, (T, QD)), normal(rng, (T, KVD)), normal(rng, (T, KVD))
+    table = ie.rope_table(2048, HD, 1e6).to(dev)
+    for plan_h in plans:
+        assert plan_h.size >= ie.attention_plan_ints(T, nc, ct)
+        plan = torch.from_numpy(plan_h).to(dev)
+        ws_n = ie.lib().ie_hip_attention_workspace_bytes(T, NH, HD, nc) // 4
+        wsbuf = torch.full((ws_n + 256,), 5.0, device=dev)
+        outbuf = torch.full((T * QD + 256,), 7.0, device=dev)
+        out = outbuf[:T * QD].view(T, QD)
+        ws = wsbuf[:ws_n]
+        dkp, dvp = to_dev(kp, dev, kvt), to_dev(vp, dev, kvt)
+        args = (to_dev(pos, dev), to_dev(seq, dev), to_dev(tables, dev), int(max_pages), nc, ct,
+                ws, plan, NH, NKV, HD)
+        if fused:
+            ie.rope_cache_attention_planned(out, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev),
+                                            dkp, dvp, table, *args)
+        else:
+            ie.attention_planned(out, to_dev(q, dev), dkp, dvp, *args)
+        torch.cuda.synchronize()
+        assert torch.all(outbuf[T * QD:] == 7.0), "wrote past out"
+        assert torch.all(wsbuf == 5.0), "the partial kernel wrote into the workspace"
+        assert torch.all(out[0] == 7.0), "a single-chunk row was written"
+        assert np.array_equal(from_dev(dkp), kp) and np.array_equal(from_dev(dvp), vp)
