@@ -377,23 +377,27 @@ void section_serve(Ctx& c) {
   const int max_batch = 16;
   std::unique_ptr<ie::BatchRunner> eng =
       ie::hip::make_batch_runner(c.cfg, c.w, max_batch, 256, size_t(1) << 34, true, c.kv);
-  const ie::hip::ServeStats one = ie::hip::serve(*eng, reqs, 1);
-  result(eng->free_pages() == eng->total_pages(), "concurrency 1: every page back at the end");
+  const ie::hip::ServeReport one = ie::hip::serve(*eng, reqs, 1);
+  result(eng->free_pages() == eng->total_pages(), "one at a time: every page back at the end");
+  bool lengths = true;
+  for (size_t i = 0; i < reqs.size(); ++i)
+    lengths = lengths && int(one.requests[i].tokens.size()) == reqs[i].gen;
+  result(lengths && one.largest_batch == 1, "one at a time: each request its own length");
   for (int conc : {4, 16}) {
-    const ie::hip::ServeStats s = ie::hip::serve(*eng, reqs, conc);
-    const ie::hip::CheckResult k = ie::hip::check_identical(s, one);
+    const ie::hip::ServeReport s = ie::hip::serve(*eng, reqs, conc);
+    const ie::hip::TokenMatch k = ie::hip::tokens_match(s, one);
     char b[200];
     std::snprintf(b, sizeof(b),
-                  "concurrency %d: %d/%d identical to one at a time (peak batch %d, %d steps, "
-                  "%.0f tok/s)%s",
-                  conc, k.identical, k.total, s.peak_batch, s.steps, s.tokens / s.seconds,
-                  k.all() ? "" : " -- first difference below");
-    result(k.all() && s.peak_batch > 1, b);
+                  "%d running at most: %d/%d identical to one at a time (largest batch %d, %d "
+                  "steps, %.0f tok/s)%s",
+                  conc, k.same, k.total, s.largest_batch, s.decode_steps,
+                  double(s.tokens()) / s.wall_s, k.all() ? "" : " -- first difference below");
+    result(k.all() && s.largest_batch > 1, b);
     if (!k.all()) std::printf("     request %d differs from token %d\n", k.first_request, k.first_token);
     result(eng->free_pages() == eng->total_pages(), "every page back at the end");
   }
-  // Admission by full-length reservation: a cache of 10 pages serves requests
-  // of 6 pages one at a time even at concurrency 4.
+  // Admission by full-length promise: a cache of 10 pages serves requests of 6
+  // pages one at a time even with 4 slots.
   {
     const size_t kv_elem = c.kv == ie::hip::KvDtype::F32 ? 4 : 2;
     std::unique_ptr<ie::BatchRunner> small = ie::hip::make_batch_runner(
@@ -403,14 +407,15 @@ void section_serve(Ctx& c) {
       q.prompt = c.tokens(80);
       q.gen = 10;  // 90 tokens: 6 pages
     }
-    const ie::hip::ServeStats s = ie::hip::serve(*small, r, 4);
-    result(s.peak_batch == 1 && s.peak_pages <= 6, "full-length reservation: one 6-page request "
-                                                   "at a time in a 10-page cache");
+    const ie::hip::ServeReport s = ie::hip::serve(*small, r, 4);
+    result(s.largest_batch == 1 && s.most_pages_in_use <= 6,
+           "full-length promise: one 6-page request at a time in a 10-page cache");
     std::vector<ie::hip::ServeRequest> big(1);
     big[0].prompt = c.tokens(90);
     big[0].gen = 80;
-    expect_error("a request larger than the cache", "more KV-cache pages than the cache has",
+    expect_error("a request larger than the cache", "KV-cache pages at full length",
                  [&] { ie::hip::serve(*small, big, 1); });
+    result(small->free_pages() == small->total_pages(), "a refused request holds no pages");
   }
 }
 
