@@ -72,6 +72,27 @@ const char* ie_hip_version(void);
 enum { IE_HIP_IMPL_AUTO = 0, IE_HIP_IMPL_VALU = 1, IE_HIP_IMPL_MFMA = 2 };
 int ie_hip_set_attention_impl(int impl);
 
+/* Process-wide operand precision of the matrix-core prefill on f16 caches, the
+ * counterpart of the reference's set_tc_fp16 (src/cuda/cuda_runner.h:31-32,
+ * src/cuda/kernels.cu:1361-1372, which picks its FP16 tensor-core prompt
+ * kernel when on):
+ *   IE_HIP_PREFILL_SINGLE (default) -- q and P enter the matrix cores as single
+ *       f16 values rounded to nearest (the reference's tensor-core rounding,
+ *       src/cuda/kernels.cu:673-674,741); errors ~6e-4 at 4,000 keys;
+ *   IE_HIP_PREFILL_SPLIT -- q and P split into hi + lo f16 halves, every
+ *       product issued twice: float32-level scores and weights (errors ~1e-6),
+ *       at twice the matrix work. bf16 caches always split.
+ * Returns the previous setting. Not synchronised with running kernels. */
+enum { IE_HIP_PREFILL_SINGLE = 0, IE_HIP_PREFILL_SPLIT = 1 };
+int ie_hip_set_prefill_rounding(int mode);
+
+/* Named ranges on the ROCTX timeline (rocprofv3 --marker-trace), the
+ * counterpart of the reference engine's NVTX ranges
+ * (src/cuda/cuda_runner.cu:22-43,349,471). Push and pop nest per thread; a
+ * null name pushes nothing. */
+void ie_hip_range_push(const char* name);
+void ie_hip_range_pop(void);
+
 /* ---------------------------------------------------------------- RoPE ---
  * Host-side RoPE table, computed with the host C library exactly as the
  * reference's CPU rope does (src/ops.cpp:37-48): for p < n_pos, i < head_dim/2,

@@ -48,6 +48,14 @@
 namespace ie::hip {
 
 /* The model shape the path reads (the reference's Config, src/config.h:10-26). */
+/* A named ROCTX range for the lifetime of the object (ie_hip_range_push/pop). */
+struct TraceRange {
+  explicit TraceRange(const char* name) { ie_hip_range_push(name); }
+  ~TraceRange() { ie_hip_range_pop(); }
+  TraceRange(const TraceRange&) = delete;
+  TraceRange& operator=(const TraceRange&) = delete;
+};
+
 struct KvConfig {
   int num_layers = 24;
   int num_heads = 14;
@@ -192,10 +200,14 @@ class KvEngine {
     if (!pages_) throw std::runtime_error(ie_hip_last_error());
     try {
       max_pages_per_seq_ = ie_pages_max_pages_per_seq(pages_);
+      int dev = 0;
+      check(hipGetDevice(&dev), "hipGetDevice");  // the device this engine's memory lives on
       hipDeviceProp_t prop{};
-      check(hipGetDeviceProperties(&prop, 0), "hipGetDeviceProperties");
+      check(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
       static const char* const kKv[] = {"", ", f16 KV cache", ", bf16 KV cache"};
-      name_ = std::string("hip, ") + prop.name + " (" + prop.gcnArchName + ")" +
+      // The marketing name is empty where the driver's id table is missing.
+      name_ = std::string("hip, ") + (prop.name[0] ? prop.name : "AMD GPU") + " (" +
+              prop.gcnArchName + ")" +
               (use_graphs_ ? ", graphs" : ", no graphs") + kKv[kv_dtype];
       check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
       check(hipEventCreateWithFlags(&staged_, hipEventDisableTiming), "hipEventCreate");
@@ -344,6 +356,12 @@ class KvEngine {
 
     cur_rows_ = T;
     cur_logit_rows_ = R;
+    // The step on the ROCTX timeline, named as the reference names its NVTX
+    // ranges (src/cuda/cuda_runner.cu:349): one prompt, one row, several rows.
+    const TraceRange range(s.prompt   ? "prefill"
+                           : !decode  ? "mixed step"
+                           : T == 1   ? "decode"
+                                      : "decode batch");
     if (s.graph) {
       auto it = graphs_.find({T, R});
       if (it == graphs_.end()) it = graphs_.emplace(std::make_pair(T, R), record(s)).first;
@@ -500,6 +518,7 @@ class KvEngine {
 
   /* Records one decode step of s.rows sequences into a graph. */
   hipGraphExec_t record(const StepInfo& s) {
+    const TraceRange range("record decode graph");
     hipGraph_t graph = nullptr;
     check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
     try {

@@ -57,6 +57,9 @@ _SIGS = {
     "ie_hip_version": (ctypes.c_char_p, []),
     "ie_hip_set_attention_impl": (_i, [_i]),
     "ie_hip_rope_table": (_i, [_vp, _i, _i, _f]),
+    "ie_hip_set_prefill_rounding": (_i, [_i]),
+    "ie_hip_range_push": (None, [ctypes.c_char_p]),
+    "ie_hip_range_pop": (None, []),
     "ie_hip_rope_and_cache": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, KvLayout, _i, _i,
                                    _i, _vp]),
     "ie_hip_attention_chunk_tokens": (_i, [_i, _i, _i]),
@@ -166,6 +169,15 @@ IMPL_AUTO, IMPL_VALU, IMPL_MFMA = 0, 1, 2
 def set_attention_impl(impl: int) -> int:
     """Process-wide attention kernel choice (AUTO / VALU / MFMA); returns the previous one."""
     return int(lib().ie_hip_set_attention_impl(impl))
+
+
+PREFILL_SINGLE, PREFILL_SPLIT = 0, 1
+
+
+def set_prefill_rounding(mode: int) -> int:
+    """Process-wide operand precision of the f16 matrix-core prefill (SINGLE: q and P
+    rounded once to f16; SPLIT: hi + lo halves); returns the previous one."""
+    return int(lib().ie_hip_set_prefill_rounding(mode))
 
 
 # ------------------------------------------------------------ kernels ----

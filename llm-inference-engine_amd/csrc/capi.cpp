@@ -1,5 +1,8 @@
 // C-ABI plumbing shared by every entry point: per-thread error messages,
-// version string, layout validation and the host RoPE table.
+// version string, the process-wide kernel switches, ROCTX trace ranges, layout
+// validation and the host RoPE table.
+#include <rocprofiler-sdk-roctx/roctx.h>
+
 #include <cmath>
 #include <string>
 #include <vector>
@@ -35,9 +38,11 @@ int check_launch(const char* kernel) {
 
 namespace {
 int g_attention_impl = IE_HIP_IMPL_AUTO;
+int g_prefill_rounding = IE_HIP_PREFILL_SINGLE;
 }
 
 int attention_impl() { return g_attention_impl; }
+int prefill_rounding() { return g_prefill_rounding; }
 
 int check_layout(const ie_kv_layout& kv, const char* who) {
   if (kv.page_size != IE_HIP_PAGE_SIZE)
@@ -65,6 +70,18 @@ int ie_hip_set_attention_impl(int impl) {
     g_attention_impl = impl;
   return prev;
 }
+
+int ie_hip_set_prefill_rounding(int mode) {
+  const int prev = g_prefill_rounding;
+  if (mode == IE_HIP_PREFILL_SINGLE || mode == IE_HIP_PREFILL_SPLIT) g_prefill_rounding = mode;
+  return prev;
+}
+
+void ie_hip_range_push(const char* name) {
+  if (name) roctxRangePushA(name);
+}
+
+void ie_hip_range_pop(void) { roctxRangePop(); }
 
 // The angle and cos/sin of src/ops.cpp:37-48, evaluated with the host libm so
 // the table equals what the reference CPU rope computes for every position.

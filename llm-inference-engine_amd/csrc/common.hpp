@@ -22,6 +22,8 @@ int check_hip(hipError_t err, const char* what);
 // Compute units of the current device (256 on MI355X; the fallback when the query fails).
 int device_compute_units();
 int check_launch(const char* kernel);
+// Process-wide operand rounding of the f16 prefill (ie_hip_set_prefill_rounding).
+int prefill_rounding();
 
 // -------------------------------------------------------- KV conversions ---
 // f16: the hardware conversion (v_cvt_f16_f32: round to nearest even,

@@ -22,6 +22,7 @@
 //   here converts its natural-log max), and decode_merge_kernel combines them:
 //   M = max m_c, L = sum l_c 2^(m_c - M), out = sum o_c 2^(m_c - M) / L.
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -474,17 +475,23 @@ size_t workspace_bytes(int T, int n_heads, int head_dim, int num_chunks) {
 }
 
 int device_compute_units() {
-  static int cus = [] {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0) {
-      (void)hipGetLastError();
-      return 256;  // MI355X
-    }
-    return n;
-  }();
-  return cus;
+  // Per device: the count of the device current on the calling thread, looked
+  // up once per device (a launch on another device must not reuse another's).
+  constexpr int kDevices = 64;
+  static std::atomic<int> known[kDevices] = {};
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256;  // no device visible (host-only callers): MI355X's count
+  }
+  if (dev >= 0 && dev < kDevices && (n = known[dev].load(std::memory_order_relaxed)) > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 256;
+  }
+  if (dev >= 0 && dev < kDevices) known[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 int decode_valu(float* out, const float* q, const void* k_pool, const void* v_pool, int T,

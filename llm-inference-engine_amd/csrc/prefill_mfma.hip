@@ -75,7 +75,7 @@ constexpr int kSegTiles = 512;             // key tiles (32,768 keys) with page 
 // taking query heads kHeadsPerWave * w .. of the KV head. kTeams teams of
 // kWaves waves split each block's key tiles (team t takes tiles kTeams s + t)
 // and merge their (m, l, O) through LDS at the end of the block.
-template <int KV, int kWaves, int kTeams>
+template <int KV, int kWaves, int kTeams, bool kSplitF16>
 __global__ void __launch_bounds__(64 * kWaves * kTeams)
 prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
                     const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
@@ -85,7 +85,8 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
-  constexpr bool kSplit = !std::is_same_v<E, _Float16>;  // hi + lo operands (bf16)
+  // hi + lo operands: always for bf16; for f16 under IE_HIP_PREFILL_SPLIT.
+  constexpr bool kSplit = kSplitF16 || !std::is_same_v<E, _Float16>;
   constexpr int kRingSteps = kTeams == 1 ? 4 : 3;  // steps of kTeams tiles in LDS
   constexpr int kRingBytes = kRingSteps * kTeams * kBufBytes;
   op ones;  // all-ones A operand: row sums of P^T on the matrix cores
@@ -495,24 +496,38 @@ constexpr int prefill_lds_bytes() {
          4 * kSegTiles;
 }
 
-template <int KV, int W, int kTeams>
-int launch_prefill_variant(const dim3 grid, float* out, const float* q, const uint16_t* kp,
-                           const uint16_t* vp, int T, const int32_t* row_pos,
-                           const int32_t* row_seq, const ie_kv_layout& kv, int n_heads,
-                           int n_kv_heads, int n_blocks, hipStream_t stream) {
+template <int KV, int W, int kTeams, bool kSplitF16>
+int launch_prefill_split(const dim3 grid, float* out, const float* q, const uint16_t* kp,
+                         const uint16_t* vp, int T, const int32_t* row_pos,
+                         const int32_t* row_seq, const ie_kv_layout& kv, int n_heads,
+                         int n_kv_heads, int n_blocks, hipStream_t stream) {
   constexpr int lds = prefill_lds_bytes<kTeams>();
   static_assert(lds - 16 * (kSegTiles + kTeams) - 4 * kSegTiles >= W * 4096 + W * 512,
                 "team exchange area must fit in the ring");
   if (lds > 65536) {  // above the default dynamic-LDS cap, within gfx950's 160 KB
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(prefill_mfma_kernel<KV, W, kTeams>),
+        reinterpret_cast<const void*>(prefill_mfma_kernel<KV, W, kTeams, kSplitF16>),
         hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (int rc = check_hip(attr, "hipFuncSetAttribute(attention_prefill_mfma)")) return rc;
   }
-  hipLaunchKernelGGL((prefill_mfma_kernel<KV, W, kTeams>), grid, dim3(64 * W * kTeams), lds,
-                     stream, out, q, kp, vp, T, row_pos, row_seq, kv.tables, kv.max_pages,
-                     kv.num_pages, n_heads, n_kv_heads, n_blocks);
+  hipLaunchKernelGGL((prefill_mfma_kernel<KV, W, kTeams, kSplitF16>), grid,
+                     dim3(64 * W * kTeams), lds, stream, out, q, kp, vp, T, row_pos, row_seq,
+                     kv.tables, kv.max_pages, kv.num_pages, n_heads, n_kv_heads, n_blocks);
   return check_launch("attention_prefill_mfma");
+}
+
+// f16 caches take q and P as single f16 values unless the process asked for the
+// split operands (ie_hip_set_prefill_rounding); bf16 caches always split.
+template <int KV, int W, int kTeams>
+int launch_prefill_variant(const dim3 grid, float* out, const float* q, const uint16_t* kp,
+                           const uint16_t* vp, int T, const int32_t* row_pos,
+                           const int32_t* row_seq, const ie_kv_layout& kv, int n_heads,
+                           int n_kv_heads, int n_blocks, hipStream_t stream) {
+  if (KV == IE_KV_F16 && prefill_rounding() == IE_HIP_PREFILL_SPLIT)
+    return launch_prefill_split<KV, W, kTeams, true>(grid, out, q, kp, vp, T, row_pos, row_seq,
+                                                     kv, n_heads, n_kv_heads, n_blocks, stream);
+  return launch_prefill_split<KV, W, kTeams, false>(grid, out, q, kp, vp, T, row_pos, row_seq,
+                                                    kv, n_heads, n_kv_heads, n_blocks, stream);
 }
 
 template <int KV>

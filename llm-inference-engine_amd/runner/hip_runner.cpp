@@ -92,12 +92,25 @@ ModelView model_view(const Weights& w) {
   return m;
 }
 
-EngineLimits limits_for(int max_batch, int max_seq_len, int num_pages) {
+EngineLimits limits_for(int max_batch, int max_seq_len, int num_pages, int logit_rows) {
   EngineLimits lim;
   lim.max_batch = max_batch;
   lim.max_seq_len = max_seq_len;
   lim.num_pages = num_pages;
+  lim.logit_rows = logit_rows;  // 0: the engine's default, max(max_batch, 16)
   return lim;
+}
+
+// Logit rows one step of a single-sequence Runner holds: every row of a
+// forward(all_logits) of up to max_tokens tokens in one step where 128 MiB of
+// logits (on the device, and again in pinned host memory) allow it -- 220 rows
+// at Qwen2.5's 151,936-token vocabulary -- so a perplexity-style forward runs
+// in steps of that many rows, not 16.
+constexpr size_t kLogitBudget = size_t(128) << 20;
+int runner_logit_rows(const Config& cfg, int max_tokens) {
+  const size_t row_bytes = size_t(std::max(cfg.vocab_size, 1)) * sizeof(float);
+  const int budget = int(std::max<size_t>(kLogitBudget / row_bytes, 16));
+  return std::min(std::max(max_tokens, 1), budget);
 }
 
 const Config& checked(const Config& cfg, const Weights& w) {
@@ -111,10 +124,11 @@ const Config& checked(const Config& cfg, const Weights& w) {
 class HipEngine final : public Runner, public BatchRunner {
  public:
   HipEngine(const Config& cfg, const Weights& w, int max_batch, int max_seq_len, int num_pages,
-            bool use_graphs, int kv_dtype)
+            bool use_graphs, int kv_dtype, int logit_rows = 0)
       : cfg_(checked(cfg, w)), dtype_(w.dtype), weight_bytes_(w.matrix_bytes()),
         num_params_(w.num_params()),
-        kv_(kv_config(cfg), limits_for(max_batch, max_seq_len, num_pages), kv_dtype, use_graphs),
+        kv_(kv_config(cfg), limits_for(max_batch, max_seq_len, num_pages, logit_rows), kv_dtype,
+            use_graphs),
         model_(kv_config(cfg), model_shape(cfg), model_view(w), kv_.limits().step_rows,
                kv_.limits().logit_rows) {
     kv_.set_body(model_.body(kv_));
@@ -306,6 +320,19 @@ class HipEngine final : public Runner, public BatchRunner {
 
 }  // namespace
 
+void set_tensor_cores(bool on) { ie_hip_set_attention_impl(on ? IE_HIP_IMPL_AUTO : IE_HIP_IMPL_VALU); }
+
+void set_tc_fp16(bool on) {
+  ie_hip_set_prefill_rounding(on ? IE_HIP_PREFILL_SINGLE : IE_HIP_PREFILL_SPLIT);
+}
+
+void set_cublas(bool on) {
+  if (on)
+    throw std::runtime_error(
+        "--cublas: there is no cuBLAS comparison path on MI355X; the dense products run on this "
+        "engine's own matrix-core kernels");
+}
+
 bool device_available() {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess) {
@@ -316,19 +343,20 @@ bool device_available() {
 }
 
 std::string device_description() {
+  int dev = 0;
   hipDeviceProp_t prop{};
-  if (hipGetDeviceProperties(&prop, 0) != hipSuccess) {
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
     (void)hipGetLastError();
     return "no HIP device";
   }
-  return std::string(prop.name) + " (" + prop.gcnArchName + ")";
+  return std::string(prop.name[0] ? prop.name : "AMD GPU") + " (" + prop.gcnArchName + ")";
 }
 
 std::unique_ptr<Runner> make_runner(const Config& cfg, const Weights& w, int max_tokens,
                                     bool use_graphs, KvDtype kv) {
   if (max_tokens < 1) throw std::runtime_error("KV cache: max_tokens must be positive");
   return std::make_unique<HipEngine>(cfg, w, /*max_batch=*/1, max_tokens, ie_pages_for(max_tokens),
-                                     use_graphs, int(kv));
+                                     use_graphs, int(kv), runner_logit_rows(cfg, max_tokens));
 }
 
 std::unique_ptr<Runner> make_runner(const Config& cfg, const Weights& w, int max_tokens,

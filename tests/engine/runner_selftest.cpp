@@ -306,6 +306,12 @@ void section_runner(Ctx& c) {
   result(gpu->position() == 48, "position advanced to 48");
   p = c.tokens(21);
   cmp("forward 21 tokens, all logits [21, vocab]", gpu->forward(p, true), cpu->forward(p, true));
+  // A long all-logits forward: one step of the prompt kernel for all 300 rows
+  // (the runner's logit rows are sized from max_tokens).
+  p = c.tokens(300);
+  cmp("forward 300 tokens, all logits [300, vocab]", gpu->forward(p, true),
+      cpu->forward(p, true));
+  result(gpu->position() == 369, "position advanced to 369");
   // Stage reports: the same names and shapes as the CPU's, in order.
   std::vector<std::string> gs, cs;
   std::vector<std::vector<float>> gd, cd;
@@ -420,6 +426,40 @@ void section_serve(Ctx& c) {
 }
 
 
+// The drop-in's `ie test-cuda` / `ie gpu-check` counterparts and kernel
+// switches (src/main.cpp:272-287,1033-1045,1207-1213).
+void section_cli(Ctx& c) {
+  std::printf("---- run_selftest / run_device_check / kernel switches\n");
+  std::fflush(stdout);
+  const int failures = ie::hip::run_selftest();
+  std::fflush(stdout);
+  result(failures == 0, "run_selftest: every kernel family against the host CPU operations");
+  const int dc = ie::hip::run_device_check();
+  std::fflush(stdout);
+  result(dc == 0, "run_device_check");
+  // set_tensor_cores(false) and set_tc_fp16(false) switch the attention kernels
+  // and the prefill rounding; a prompt's logits must stay within the bar of
+  // the CPU Runner either way, and the switches restore.
+  std::unique_ptr<ie::Runner> cpu = ie::make_cpu_runner(c.cfg, c.w, 256);
+  const std::vector<int32_t> prompt = c.tokens(40);
+  const std::vector<float> want = cpu->forward(prompt);
+  for (const bool tc : {false, true})
+    for (const bool fp16 : {false, true}) {
+      ie::hip::set_tensor_cores(tc);
+      ie::hip::set_tc_fp16(fp16);
+      std::unique_ptr<ie::Runner> gpu = ie::hip::make_runner(c.cfg, c.w, 256, true, c.kv);
+      const double e = rel_err(gpu->forward(prompt), want);
+      char b[160];
+      std::snprintf(b, sizeof(b), "tensor_cores %d, tc_fp16 %d: 40-token prompt logits rel %.2e",
+                    int(tc), int(fp16), e);
+      result(e <= c.tol, b);
+    }
+  ie::hip::set_tensor_cores(true);
+  ie::hip::set_tc_fp16(true);
+  ie::hip::set_cublas(false);
+  expect_error("set_cublas(true)", "no cuBLAS", [] { ie::hip::set_cublas(true); });
+}
+
 void section_checkpoint(Ctx& c, const std::string& dir) {
   std::printf("---- checkpoint %s\n", dir.c_str());
   const ie::Config cfg = ie::load_config(dir + "/config.json");
@@ -490,6 +530,7 @@ int main(int argc, char** argv) {
       section_runner(c);
       section_invariance(c);
       section_serve(c);
+      section_cli(c);
     }
   } catch (const std::exception& e) {
     std::printf("FAIL exception: %s\n", e.what());

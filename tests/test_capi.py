@@ -113,3 +113,19 @@ def test_chunk_helpers(ie):
     assert ie.attention_chunk_tokens(1, 1, ie.KV_F32) == 32
     n = ie.lib().ie_hip_attention_workspace_bytes(64, 14, 64, 8)
     assert n >= 64 * 14 * 8 * 66 * 4
+
+
+def test_switches_and_trace_ranges(ie):
+    """The process-wide switches return the previous setting and ignore unknown values;
+    ROCTX ranges push and pop without a device (and a null name pushes nothing)."""
+    assert ie.set_prefill_rounding(ie.PREFILL_SPLIT) == ie.PREFILL_SINGLE
+    assert ie.set_prefill_rounding(7) == ie.PREFILL_SPLIT  # unknown: kept
+    assert ie.set_prefill_rounding(ie.PREFILL_SINGLE) == ie.PREFILL_SPLIT
+    assert ie.set_attention_impl(ie.IMPL_VALU) == ie.IMPL_AUTO
+    assert ie.set_attention_impl(ie.IMPL_AUTO) == ie.IMPL_VALU
+    L = ie.lib()
+    L.ie_hip_range_push(b"outer")
+    L.ie_hip_range_push(b"inner")
+    L.ie_hip_range_push(None)
+    L.ie_hip_range_pop()
+    L.ie_hip_range_pop()

@@ -264,3 +264,31 @@ def test_few_keys_far_apart_values(ie, O, dev, kv):
     err = float(np.abs(got[:16] - want[:16]).max())
     assert err <= 2e-3, f"rows 0-15: max abs error {err:.3e}"
     check(O, got, want, kvt, "few keys, far-apart values")
+
+
+def test_f16_split_rounding_mode(ie, O, dev):
+    """ie_hip_set_prefill_rounding (the counterpart of the reference's set_tc_fp16):
+    PREFILL_SPLIT gives an f16 cache's prefill hi + lo operands, float32-level
+    results (the bf16 path's ~1e-6); PREFILL_SINGLE (the default) rounds q and P once
+    (~1e-4). Both within the 2e-3 bound; the switch restores."""
+    kvt = KVS["f16"]
+    rng = np.random.default_rng(48)
+    tables, max_pages, num_pages = make_tables([1000], rng)
+    kp, vp = kv_pool(rng, num_pages, kvt, O), kv_pool(rng, num_pages, kvt, O)
+    row_pos = np.arange(1000, dtype=np.int32)
+    row_seq = np.zeros(1000, np.int32)
+    q = normal(rng, (1000, QD))
+    want = O.paged_attention(q, kp, vp, kvt, row_pos, row_seq, tables, max_pages, NH, NKV, HD,
+                             threads=8)
+    errs = {}
+    for mode in (ie.PREFILL_SPLIT, ie.PREFILL_SINGLE):
+        prev = ie.set_prefill_rounding(mode)
+        try:
+            got = gpu_prefill(ie, dev, q, kp, vp, kvt, row_pos, row_seq, tables, max_pages)
+        finally:
+            ie.set_prefill_rounding(prev)
+        errs[mode] = float(np.abs(got - want).max())
+    assert errs[ie.PREFILL_SPLIT] <= 2e-5, errs
+    assert errs[ie.PREFILL_SINGLE] <= 2e-3, errs
+    assert errs[ie.PREFILL_SPLIT] < errs[ie.PREFILL_SINGLE], errs
+    assert ie.set_prefill_rounding(ie.PREFILL_SINGLE) == ie.PREFILL_SINGLE
