@@ -22,12 +22,17 @@ The default line also carries:
   probe / ceiling_gbs  hand-written read kernels (llm-inference-engine_amd/probe): a 70 MB
                        and a 256 MB contiguous stream over rotated buffers, and the page
                        walk of this very batch with no arithmetic;
-  config2_append       the RoPE + paged append at 64 and 131,072 rows per launch;
-  config5_prefill      the 4,000-token prefill's MFMA fraction;
+  plan_off             the same call with the work list located by the kernel, and
+                       host_plan_build_us, the host's cost of the list per step;
+  config2_append       the RoPE + paged append at 64 and 131,072 rows per launch, and a
+                       device copy's read + write rate (its ceiling) from the same run;
+  config4_decode       the long-context decode (24 layers, batch 1, 32k, bf16) per layer;
+  config5_prefill      the 4,000-token prefill's MFMA fraction and the mixed step;
   cpu_baseline         the reference's own CPU attention (oracle/_ref: src/ops.cpp +
                        src/threadpool.cpp, -O3 -mavx2 -mfma) on the same batch, rows
                        gathered to contiguous fp32 first (timed apart), with the host's
-                       physical core count and the threads used.
+                       physical core count and the threads used; its GB/s counts the
+                       CPU's own fp32-cache bytes.
 
 Other configs print the same JSON shape for the tables in DESIGN.md:
   --config 1  the reference's own CPU case (one layer, 512 positions, fp32), GPU and CPU
@@ -174,8 +179,11 @@ def cpu_baseline_decode(O, lens, k_host, v_host, tables, kv, q_host, budget_s=10
             break
     t = float(np.median(attn_s))
     return {
-        "value": round(decode_bytes(lens, KV_BYTES[kv]) / t / 1e9, 3),
+        # The CPU's own algorithmic bytes: its cache is fp32 (4 bytes per element)
+        # whatever the GPU pools hold.
+        "value": round(decode_bytes(lens, 4) / t / 1e9, 3),
         "unit": "GB/s",
+        "bytes": "fp32 cache (the CPU path has no 16-bit cache)",
         "cores": cores,
         "threads": cores,
         "physical_cores": O.physical_cores(),
@@ -258,8 +266,9 @@ def cpu_baseline_long(O, k_pools, v_pools, tabs, q, L, kv, layers, budget_s=8.0)
         if time.perf_counter() - t_start >= budget_s and n >= 2:
             break
     t = float(np.median(attn)) * layers
-    per_layer = 2 * KVD * KV_BYTES[kv] * L + 2 * QD * 4 + 4 * (L // PAGE) + 8
+    per_layer = 2 * KVD * 4 * L + 2 * QD * 4 + 4 * (L // PAGE) + 8  # fp32 cache bytes
     return {"value": round(layers * per_layer / t / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "bytes": "fp32 cache (the CPU path has no 16-bit cache)",
             "threads": cores, "physical_cores": O.physical_cores(),
             "kind": "reference" if O.ref_available() else "port",
             "sample": f"{n} layers' attention over 32,768 positions (gather to contiguous fp32 "
@@ -405,6 +414,36 @@ def bench_decode(args, torch, ie, O):
     timing = dict(TIMING)
     nbytes = decode_bytes(lens, KV_BYTES[kv])
     gbs = nbytes / (ms * 1e-3) / 1e9
+    plan_extra = {}
+    if d_plan is not None:
+        # The same call with the work list located by the kernel instead (no host list),
+        # and what building the list costs the host per step: ie_hip_attention_plan over
+        # host arrays, called through ctypes (its call overhead included).
+        def step_unplanned(i):
+            l = i % args.layers
+            ie.attention(out, q, k_pools[l], v_pools[l], d_pos, d_seq, d_tab, max_pages, nc,
+                         ct, ws, NH, NKV, HD)
+
+        ms_off = time_steps(torch, step_unplanned, args.steps, args.warmup, stream)
+        pos_h = np.ascontiguousarray(lens - 1, np.int32)
+        seq_h = np.arange(B, dtype=np.int32)
+        tab_h = np.ascontiguousarray(tables, np.int32)
+        n_plan = int(ie.lib().ie_hip_attention_plan_ints(B, nc, ct))
+        plan_h = np.zeros(n_plan, np.int32)
+        ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+        builds = []
+        for _ in range(7):
+            t0 = time.perf_counter()
+            for _ in range(200):
+                ie.lib().ie_hip_attention_plan(ptr(plan_h), n_plan, B, ptr(pos_h), ptr(seq_h),
+                                               ptr(tab_h), B, max_pages, nc, ct)
+            builds.append((time.perf_counter() - t0) / 200)
+        gbs_off = nbytes / (ms_off * 1e-3) / 1e9
+        plan_extra = {"plan_off": {"ms_per_step": round(ms_off, 5), "gbs": round(gbs_off, 2),
+                                   "frac": round(gbs_off / HBM_PEAK_GBS, 4),
+                                   "note": "ie_hip_attention: the kernel locates each "
+                                           "workgroup's (row, chunk) and page ids itself"},
+                      "host_plan_build_us": round(float(np.median(builds)) * 1e6, 2)}
 
     # Warm, for reference only: the same call repeated on one layer's pools, so the
     # pages it reads (70 MB) stay in the 256 MB Infinity Cache (MALL) between calls.
@@ -438,6 +477,7 @@ def bench_decode(args, torch, ie, O):
                      "us_per_launch": round(ms * 1e3, 3)},
         "algorithmic_bytes_per_step": nbytes,
         "timing": timing,
+        **plan_extra,
         "warm_mall": {"ms_per_step": round(ms_warm, 5),
                       "gbs": round(nbytes / (ms_warm * 1e-3) / 1e9, 2),
                       "note": "one layer's pools repeated: pages resident in the Infinity Cache; "
@@ -496,7 +536,8 @@ def bench_append(args, torch, ie, O):
             per_row = (1024 + 2 * KVD * KV_BYTES[kv] + 8 + 4) + (2 * QD * 4 if with_q else 0)
             sweep.append({"rows": rows, "with_q": with_q, "us_per_launch": round(ms * 1e3, 3),
                           "gbs": round(rows * per_row / (ms * 1e-3) / 1e9, 2)})
-    head = [s for s in sweep if s["rows"] == 64 and s["with_q"] == (args.append_q == "on")][0]
+    mode = [s for s in sweep if s["with_q"] == (args.append_q == "on")] or sweep
+    head = ([s for s in mode if s["rows"] == 64] or mode)[0]
     res = {
         "metric": "paged RoPE+KV append GB/s at batch 64 (K/V only), 1 GPU",
         "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -512,7 +553,7 @@ def bench_append(args, torch, ie, O):
                      "us_per_launch": head["us_per_launch"]},
         "sweep": sweep,
     }
-    if not args.no_cpu:
+    if not args.no_cpu and 64 in rows_list:
         res["cpu_baseline"] = cpu_baseline_append(O, *cpu_in, kv)
     return res
 
@@ -674,11 +715,13 @@ def bench_mixed(args, torch, ie, O):
         ie.attention(d_out, dq, k_pool, v_pool, d_pos, d_seq, d_tab, max_pages, nc, ct, ws, NH,
                      NKV, HD)
 
-    # The prompt and the decode rows touch different sequences (different pages), so the
-    # decode half runs on a second stream (default priority), forked from and joined
-    # back into the launch stream: in the recorded graph the two halves are parallel
-    # branches, and the decode rows' short kernels fill the compute units the prefill's
-    # one workgroup per unit leaves idle.
+    # The step as the engine runs it: one stream, the prefill then the decode rows
+    # (step_serial, the reported ms_per_step). Beside it, a composition bound: the
+    # prompt and the decode rows touch different sequences (different pages), so the
+    # decode half can run on a second stream (default priority), forked from and
+    # joined back into the launch stream -- two parallel branches of one graph, the
+    # decode rows' short kernels filling the compute units the prefill's one
+    # workgroup per unit leaves idle. No engine path schedules a step that way.
     side = torch.cuda.Stream(device=dev)
 
     def step(i):
@@ -693,8 +736,8 @@ def bench_mixed(args, torch, ie, O):
         prefill(i)
         decode(i)
 
-    ms = time_steps(torch, step, args.steps, args.warmup, stream)
-    ms_serial = time_steps(torch, step_serial, args.steps, args.warmup, stream)
+    ms_branches = time_steps(torch, step, args.steps, args.warmup, stream)
+    ms = time_steps(torch, step_serial, args.steps, args.warmup, stream)
     ms_pf = time_steps(torch, prefill_attn, args.steps, args.warmup, stream)
     ms_dec = time_steps(torch, decode, args.steps, args.warmup, stream)
     flops = 4 * NH * HD * P * (P + 1) // 2
@@ -712,7 +755,10 @@ def bench_mixed(args, torch, ie, O):
         "config": {"workload": "config 5: 48 decode rows (L~U[256,2048]) + one 4,000-token "
                                "prefill into fresh pages after 25% page churn, one layer",
                    "kv_dtype": kv, "chunk_tokens": ct, "seed": args.seed},
-        "ms_per_step_one_stream": round(ms_serial, 5),
+        "step": "one stream: the prefill, then the decode rows (the engine's order)",
+        "ms_per_step_two_branches": round(ms_branches, 5),
+        "two_branches_note": "a kernel-composition bound, not an engine path: the decode "
+                             "half on a parallel graph branch beside the prefill",
         "prefill_attention_ms": round(ms_pf, 5),
         "prefill_tflops": round(tflops, 2),
         "decode_part_ms": round(ms_dec, 5),
@@ -879,8 +925,18 @@ def extra_targets(args, torch, ie, O):
     sub.append_rows, sub.append_q = [64, 131072], "off"
     app = bench_append(sub, torch, ie, O)
     pts = {s["rows"]: s for s in app["sweep"] if not s["with_q"]}
+    copy_gbs = copy_probe(torch)
     mix = bench_mixed(sub, torch, ie, O)
+    sub4 = copy.copy(sub)
+    sub4.steps = max(10, min(args.steps, 50))
+    lng = bench_long(sub4, torch, ie, O)
     return {
+        "config4_decode": {
+            "us_per_layer": lng["us_per_layer"], "ms_per_step": lng["ms_per_step"],
+            "gbs": lng["roofline"]["achieved"], "frac": lng["roofline"]["frac"],
+            "traffic_per_step": lng["roofline"]["traffic"],
+            "algorithmic_bytes_per_step": lng["algorithmic_bytes_per_step"],
+            "kernel": lng["roofline"]["kernel"], "layer_calls": lng["config"]["layer_calls"]},
         "config2_append": {
             "rows_64": {"us_per_launch": pts[64]["us_per_launch"], "gbs": pts[64]["gbs"],
                         "frac": round(pts[64]["gbs"] / HBM_PEAK_GBS, 4)},
@@ -888,11 +944,17 @@ def extra_targets(args, torch, ie, O):
                             "gbs": pts[131072]["gbs"],
                             "frac": round(pts[131072]["gbs"] / HBM_PEAK_GBS, 4)},
             "target_frac": 0.60, "bytes_per_row": 1548,
+            # The append reads 2/3 and writes 1/3 of its bytes: a device-to-device copy
+            # (read + write, 2 GiB) measured in the same run is its ceiling.
+            "copy_gbs": copy_gbs,
+            "frac_of_copy": round(pts[131072]["gbs"] / copy_gbs, 4),
             "kernel": "rope_append_kernel (ie_hip_rope_and_cache, K/V only)"},
         "config5_prefill": {
             "us_per_launch": mix["roofline"]["us_per_launch"],
             "tflops": mix["roofline"]["achieved"], "frac": mix["roofline"]["frac"],
-            "mixed_step_ms": mix["ms_per_step"], "decode_part_gbs": mix["decode_part_gbs"],
+            "mixed_step_ms": mix["ms_per_step"],
+            "mixed_step_two_branches_ms": mix["ms_per_step_two_branches"],
+            "decode_part_gbs": mix["decode_part_gbs"],
             "kernel": mix["roofline"]["kernel"]},
     }
 
@@ -1172,6 +1234,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true", help="config 2: rows-per-launch sweep")
+    ap.add_argument("--append-rows", default=None,
+                    help="config 2: comma-separated rows per launch to time instead of the "
+                         "default (64, or the sweep); one size alone gives per-dispatch "
+                         "counters of that size")
     ap.add_argument("--plan", choices=["on", "off"], default="on",
                     help="configs 3 and 4: the decode work list built on the host "
                          "(ie_hip_attention_plan), as the engine does, or located by the kernel")
@@ -1191,6 +1257,8 @@ def main():
                     help="only the device copy (the plain copy kernel that rocprofv3 byte "
                          "counters are calibrated on)")
     args = ap.parse_args()
+    if args.append_rows:
+        args.append_rows = [int(x) for x in args.append_rows.split(",")]
     global EAGER
     EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

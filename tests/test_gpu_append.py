@@ -115,3 +115,22 @@ def test_config2_full_size(ie, O, dev):
     run_case(ie, O, dev, kvt, tables, max_pages, num_pages, row_seq, row_pos,
              normal(rng, (64, QD)), normal(rng, (64, KVD)), normal(rng, (64, KVD)), rng,
              table_positions=4096)
+
+
+@pytest.mark.parametrize("kv", list(KVS))
+@pytest.mark.parametrize("with_q", [False, True])
+def test_large_launch(ie, O, dev, kv, with_q):
+    """A launch of over a million threads: 22,003 rows of 128 sequences, every slot
+    distinct, rows in shuffled order (so neighbouring threads write scattered pages);
+    every byte of both pools and q checked."""
+    rng = np.random.default_rng(9 + KVS[kv] + 3 * with_q)
+    n_seq, per_seq, T = 128, 172, 22003
+    lens = [per_seq] * n_seq
+    tables, max_pages, num_pages = make_tables(lens, rng, extra_pages=5)
+    slots = np.array([(s, p) for s in range(n_seq) for p in range(per_seq)], np.int32)
+    slots = slots[rng.permutation(len(slots))[:T]]
+    row_seq = np.ascontiguousarray(slots[:, 0])
+    row_pos = np.ascontiguousarray(slots[:, 1])
+    run_case(ie, O, dev, KVS[kv], tables, max_pages, num_pages, row_seq, row_pos,
+             normal(rng, (T, QD)), normal(rng, (T, KVD)), normal(rng, (T, KVD)), rng,
+             with_q=with_q)
