@@ -942,7 +942,9 @@ def extra_targets(args, torch, ie, O):
                         "frac": round(pts[64]["gbs"] / HBM_PEAK_GBS, 4)},
             "rows_131072": {"us_per_launch": pts[131072]["us_per_launch"],
                             "gbs": pts[131072]["gbs"],
-                            "frac": round(pts[131072]["gbs"] / HBM_PEAK_GBS, 4)},
+                            "frac": round(pts[131072]["gbs"] / HBM_PEAK_GBS, 4),
+                            "traffic": traffic_from_profiles("append_131072", "f16", "f16",
+                                                             sub)},
             "target_frac": 0.60, "bytes_per_row": 1548,
             # The append reads 2/3 and writes 1/3 of its bytes: a device-to-device copy
             # (read + write, 2 GiB) measured in the same run is its ceiling.
