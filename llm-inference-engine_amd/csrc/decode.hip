@@ -236,9 +236,9 @@ decode_partial_valu(float* __restrict__ out, float* __restrict__ part_o,
 // chunks that saw no position (m = -inf) are identities that every merge
 // passes through unchanged, so padding the tree to any width changes nothing.
 //
-// A workgroup takes one (head, row) and a slice of 64/S output dims (S = 1, 2
-// or 4 slices, more slices when rows x heads alone would leave compute units
-// idle). In a wave, lane = (dim quad, block lane): the slice's Q quads of
+// A workgroup takes one (head, row) and a slice of 64/S output dims (S = 1 to
+// 16 slices, more slices when rows x heads alone would leave compute units
+// idle or the row has more chunks than one wave's lanes hold). In a wave, lane = (dim quad, block lane): the slice's Q quads of
 // float4, each over CL = 64/Q consecutive lanes; block lane i of wave w owns
 // block w * CL + i and loads its 8 chunks at once. The tree runs over the
 // block lanes -- node (b, b + k) forms in b's lane from lane b + k, a VALU
@@ -313,15 +313,35 @@ __device__ __forceinline__ void lane_tree(MergeAcc& acc) {
   }
 }
 
-// Q = dim quads per slice (16, 8 or 4 for S = 1, 2, 4); blockIdx = (head, row, slice).
+// Q = dim quads per slice (16, 8, 4, 2 or 1 for S = 16 / Q = 1 .. 16 slices).
+// One slice: blockIdx = (head, row). Several slices: a 1-D grid in which all
+// slices of one (row, head) run on the same XCD. MI355X hands workgroup w to
+// XCD w mod 8, so workgroup w = x + 8 j takes (row, head) pair x + 8 (j / S)
+// and slice j % S. The slices share the 128-byte lines of their pair's
+// partials and all of its (m, l) values; on one XCD those lines come from HBM
+// once and from that XCD's L2 after, where slices spread over four XCDs
+// fetched every line four times. Workgroups past the last pair leave at once.
+// Where workgroups land changes no sum, only the traffic.
 template <int Q>
 __global__ void __launch_bounds__(64 * kMergeMaxWaves)
 decode_merge_kernel(float* __restrict__ out, const float* __restrict__ part_o,
                     const float* __restrict__ part_ml, const int32_t* __restrict__ row_pos,
-                    int n_heads, int num_chunks, int chunk_tokens) {
-  constexpr int HD = 64, CL = 64 / Q;
+                    int T, int n_heads, int num_chunks, int chunk_tokens) {
+  constexpr int HD = 64, CL = 64 / Q, S = 16 / Q;
   __shared__ MergeAcc red[kMergeMaxWaves][Q];
-  const int h = blockIdx.x, t = blockIdx.y, s = blockIdx.z;
+  int h, t, s;
+  if constexpr (S == 1) {
+    h = blockIdx.x;
+    t = blockIdx.y;
+    s = 0;
+  } else {
+    const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+    const int pair = x + 8 * (j / S);
+    if (pair >= T * n_heads) return;
+    h = pair % n_heads;
+    t = pair / n_heads;
+    s = j % S;
+  }
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
   const int qd = lane / CL, bl = lane % CL;
   const int p = row_pos[t];
@@ -442,11 +462,13 @@ int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T,
   const int waves = (blocks + blocks_per_wave - 1) / blocks_per_wave;
   if (waves > kMergeMaxWaves)
     return fail(IE_HIP_EINVAL, "attention: more than 8,192 chunks per row");
-  const dim3 grid(n_heads, T, slices), block(64 * waves);
+  // Several slices: 8 XCD lanes x ceil(pairs / 8) pairs each x slices (see the kernel).
+  const dim3 grid = slices == 1 ? dim3(n_heads, T) : dim3(8 * ((pairs + 7) / 8) * slices);
+  const dim3 block(64 * waves);
 #define IE_MERGE_CASE(S)                                                                     \
   case S:                                                                                    \
     hipLaunchKernelGGL((decode_merge_kernel<16 / S>), grid, block, 0, stream, out, ws.part_o, \
-                       ws.part_ml, row_pos, n_heads, num_chunks, chunk_tokens);              \
+                       ws.part_ml, row_pos, T, n_heads, num_chunks, chunk_tokens);           \
     break;
   switch (slices) {
     IE_MERGE_CASE(1)
