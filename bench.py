@@ -709,11 +709,30 @@ def bench_mixed(args, torch, ie, O):
         ie.attention_prefill(p_out, pq, k_pool, v_pool, p_pos, p_seq, d_tab, max_pages, NH, NKV,
                              HD)
 
-    def decode(i):
+    # The decode rows as the engine's decode step runs them (KvEngine::run): RoPE +
+    # append folded into the attention launch, reading a host-built work list, where the
+    # library offers that (16-bit caches); else the two calls. The list is built once
+    # (the positions do not change between steps; the engine builds it every step, its
+    # host cost is the config-3 line's host_plan_build_us).
+    fused = ie.rope_cache_attention_supported(KV_CODES[kv], NH, NKV, HD, ct)
+    d_plan = None
+    if fused:
+        d_plan = torch.from_numpy(ie.attention_plan(
+            d_pos.cpu().numpy(), d_seq.cpu().numpy(),
+            d_tab.cpu().numpy().reshape(pool.max_batch, max_pages), nc, ct)).to(dev)
+
+    def decode_two_calls(i):
         ie.rope_and_cache(dq, dk, dv, k_pool, v_pool, table, d_pos, d_seq, d_tab, max_pages,
                           NH, NKV, HD)
         ie.attention(d_out, dq, k_pool, v_pool, d_pos, d_seq, d_tab, max_pages, nc, ct, ws, NH,
                      NKV, HD)
+
+    def decode(i):
+        if not fused:
+            decode_two_calls(i)
+            return
+        ie.rope_cache_attention_planned(d_out, dq, dk, dv, k_pool, v_pool, table, d_pos, d_seq,
+                                        d_tab, max_pages, nc, ct, ws, d_plan, NH, NKV, HD)
 
     # The step as the engine runs it: one stream, the prefill then the decode rows
     # (step_serial, the reported ms_per_step). Beside it, a composition bound: the
@@ -740,6 +759,7 @@ def bench_mixed(args, torch, ie, O):
     ms = time_steps(torch, step_serial, args.steps, args.warmup, stream)
     ms_pf = time_steps(torch, prefill_attn, args.steps, args.warmup, stream)
     ms_dec = time_steps(torch, decode, args.steps, args.warmup, stream)
+    ms_dec2 = time_steps(torch, decode_two_calls, args.steps, args.warmup, stream) if fused else ms_dec
     flops = 4 * NH * HD * P * (P + 1) // 2
     # Dense matrix peak of the type the prefill tiles run in: the 16-bit MFMA for
     # f16/bf16 caches, the fp32 MFMA for f32 caches (MI355X published figures).
@@ -763,6 +783,9 @@ def bench_mixed(args, torch, ie, O):
         "prefill_tflops": round(tflops, 2),
         "decode_part_ms": round(ms_dec, 5),
         "decode_part_gbs": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2),
+        "decode_part_calls": ("rope_cache_attention_planned (the engine's decode step)" if fused
+                              else "rope_and_cache + attention"),
+        "decode_part_two_calls_ms": round(ms_dec2, 5),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": mfma_peak,
                      "unit": "TFLOP/s", "frac": round(tflops / mfma_peak, 4), "traffic": None,
                      "kernel": ("prefill_mfma_f32_kernel" if kv == "f32" else "prefill_mfma_kernel")
