@@ -69,6 +69,7 @@ constexpr int kHeadsPerWave = 1;           // query heads per wave (2 measured s
 static_assert(kHeadsPerWave == 1, "the team exchange hands over one head per wave");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;           // log2 headroom of the lazily raised softmax max
+constexpr float kSumMax = 16384.0f;        // largest tile row sum taken without a new max
 constexpr int kSegTiles = 512;             // key tiles (32,768 keys) with page ids in LDS at once
 
 // kWaves = group / kHeadsPerWave waves per team (rounded up), wave w of a team
@@ -226,13 +227,17 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
 
     // Per head: running max (base 2), the row's sum of weights, and O^T
     // (lane (g, r) holds row r, dims 16 mt + 4g + e).
+    // nref: every entry -(the reference max, 0 while m = -inf), the value the S
+    // accumulators start from; kept across steps and changed only when m is raised.
     float m[kHeadsPerWave];
-    f32x4 lacc[kHeadsPerWave];  // every entry: the row's sum of weights
+    float lsum[kHeadsPerWave];  // the row's sum of weights
+    f32x4 nref[kHeadsPerWave];
     f32x4 o[kHeadsPerWave][4];
 #pragma unroll
     for (int hh = 0; hh < kHeadsPerWave; ++hh) {
       m[hh] = -INFINITY;
-      lacc[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+      lsum[hh] = 0.0f;
+      nref[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) o[hh][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -315,15 +320,12 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
           }
           // The accumulators start at -mref (the row's reference max, 0 before any
           // visible key), so the products come out as s - mref directly.
-          float mref[kHeadsPerWave];
-#pragma unroll
-          for (int hh = 0; hh < kHeadsPerWave; ++hh) mref[hh] = m[hh] == -INFINITY ? 0.0f : m[hh];
           f32x4 s[kHeadsPerWave][4];
 #pragma unroll
           for (int kt4 = 0; kt4 < 4; ++kt4)
 #pragma unroll
             for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-              f32x4 acc = {-mref[hh], -mref[hh], -mref[hh], -mref[hh]};
+              f32x4 acc = nref[hh];
 #pragma unroll
               for (int ks = 0; ks < 2; ++ks) {
                 acc = M::mma(ka[kt4][ks], qhi[hh][ks], acc);
@@ -346,71 +348,109 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
           }
           // Online softmax per head on s - mref; P^T operands per 32-key group kg:
           // slots 0-3 = keys 32kg + 4g + e (group 2kg), slots 4-7 = keys 32kg + 16 +
-          // 4g + e. The reference max m is raised lazily: weights are 2^(s - m) with
-          // m the row's max when it was last raised, and O and l are rescaled only
-          // when some row of the wave sees its max grow past m + kLazyMax (so weights
-          // stay below 2^kLazyMax, in range for f16 and, split hi + lo, carried at
-          // full precision in bf16). The row sums l come from the matrix cores
-          // (below), from the same operands as O.
+          // 4g + e. The reference max mref is raised lazily: weights are 2^(s - mref)
+          // with mref the row's max when it was last raised, and O and l are rescaled
+          // only when the reference has to move.
+          //   Until every row of the wave has a reference (its first visible tile),
+          //   each tile's max is taken and the reference raised when a row's max
+          //   passes mref + kLazyMax (weights then <= 2^kLazyMax).
+          //   After that (single-rounded f16 operands; split hi + lo operands take
+          //   the max on every tile) a tile's weights are formed against the standing reference
+          //   without a max, and the tile's row sums (from the matrix cores, from the
+          //   same rounded operands as O) tell whether it may: while every row's sum
+          //   is <= kSumMax, so is every weight -- in range for f16, whose largest
+          //   value is 65504, and at a magnitude where rounding is relative, as it
+          //   is at any normal magnitude. A larger sum (or an f16 weight rounded to
+          //   inf) sends the tile through the max and the raise above, and its
+          //   weights are formed again. The row sums l come from the matrix cores.
           op phi[kHeadsPerWave][2], plo[kHeadsPerWave][2];
 #pragma unroll
           for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-            const f32x4(&sh)[4] = s[hh];
-            float mx = max_nn(max3_nn(max3_nn(sh[0][0], sh[0][1], sh[0][2]),
-                                      max3_nn(sh[0][3], sh[1][0], sh[1][1]),
-                                      max3_nn(sh[1][2], sh[1][3], sh[2][0])),
-                              max3_nn(max3_nn(sh[2][1], sh[2][2], sh[2][3]),
-                                      max3_nn(sh[3][0], sh[3][1], sh[3][2]), sh[3][3]));
-            mx = group_max4(mx);  // the tile's row max, relative to mref
-            // m = -inf (nothing visible yet) always counts as growth when mx is finite.
-            const bool grow = mx > (m[hh] == -INFINITY ? -INFINITY : kLazyMax);
-            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-              const float m_new = fmaxf(m[hh], mref[hh] + mx);
-              // m = -inf (nothing seen yet): the old terms are all zero
-              const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m[hh] - m_new);
-              lacc[hh] *= corr;
+            auto raise = [&]() {
+              const f32x4(&sh)[4] = s[hh];
+              float mx = max_nn(max3_nn(max3_nn(sh[0][0], sh[0][1], sh[0][2]),
+                                        max3_nn(sh[0][3], sh[1][0], sh[1][1]),
+                                        max3_nn(sh[1][2], sh[1][3], sh[2][0])),
+                                max3_nn(max3_nn(sh[2][1], sh[2][2], sh[2][3]),
+                                        max3_nn(sh[3][0], sh[3][1], sh[3][2]), sh[3][3]));
+              mx = group_max4(mx);  // the tile's row max, relative to mref
+              // m = -inf (nothing visible yet) always counts as growth when mx is finite.
+              const bool grow = mx > (m[hh] == -INFINITY ? -INFINITY : kLazyMax);
+              if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+                const float mref = -nref[hh][0];
+                const float m_new = fmaxf(m[hh], mref + mx);
+                // m = -inf (nothing seen yet): the old terms are all zero
+                const float corr = m_new == -INFINITY ? 1.0f : exp2_weight(m[hh] - m_new);
+                lsum[hh] *= corr;
 #pragma unroll
-              for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
-              m[hh] = m_new;
-              // Re-reference this tile's scores to the new max.
-              const float shift = (m_new == -INFINITY ? 0.0f : m_new) - mref[hh];
+                for (int mt = 0; mt < 4; ++mt) o[hh][mt] *= corr;
+                m[hh] = m_new;
+                // Re-reference this tile's scores to the new max.
+                const float ref = m_new == -INFINITY ? 0.0f : m_new;
+                const float shift = ref - mref;
 #pragma unroll
-              for (int kt4 = 0; kt4 < 4; ++kt4) s[hh][kt4] -= shift;
-            }
-#pragma unroll
-            for (int kg = 0; kg < 2; ++kg)
-#pragma unroll
-              for (int e = 0; e < 4; e += 2) {
-                const float pa0 = exp2_weight(s[hh][2 * kg][e]);
-                const float pa1 = exp2_weight(s[hh][2 * kg][e + 1]);
-                const float pb0 = exp2_weight(s[hh][2 * kg + 1][e]);
-                const float pb1 = exp2_weight(s[hh][2 * kg + 1][e + 1]);
-                E h0, h1, l0, l1;
-                if constexpr (kSplit) {
-                  split16x2(pa0, pa1, h0, h1, l0, l1);
-                  plo[hh][kg][e] = l0;
-                  plo[hh][kg][e + 1] = l1;
-                } else {
-                  round16x2(pa0, pa1, h0, h1);
-                }
-                phi[hh][kg][e] = h0;
-                phi[hh][kg][e + 1] = h1;
-                if constexpr (kSplit) {
-                  split16x2(pb0, pb1, h0, h1, l0, l1);
-                  plo[hh][kg][4 + e] = l0;
-                  plo[hh][kg][5 + e] = l1;
-                } else {
-                  round16x2(pb0, pb1, h0, h1);
-                }
-                phi[hh][kg][4 + e] = h0;
-                phi[hh][kg][5 + e] = h1;
+                for (int kt4 = 0; kt4 < 4; ++kt4) s[hh][kt4] -= shift;
+                nref[hh] = f32x4{-ref, -ref, -ref, -ref};
               }
-            // Row sums: an all-ones A operand against P^T puts sum_k P[r][k] of the
-            // tile's 32-key group in every entry of lane r's accumulator.
+            };
+            auto weights = [&]() {
 #pragma unroll
-            for (int kg = 0; kg < 2; ++kg) {
-              lacc[hh] = M::mma(ones, phi[hh][kg], lacc[hh]);
-              if constexpr (kSplit) lacc[hh] = M::mma(ones, plo[hh][kg], lacc[hh]);
+              for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                  const float pa0 = exp2_weight(s[hh][2 * kg][e]);
+                  const float pa1 = exp2_weight(s[hh][2 * kg][e + 1]);
+                  const float pb0 = exp2_weight(s[hh][2 * kg + 1][e]);
+                  const float pb1 = exp2_weight(s[hh][2 * kg + 1][e + 1]);
+                  E h0, h1, l0, l1;
+                  if constexpr (kSplit) {
+                    split16x2(pa0, pa1, h0, h1, l0, l1);
+                    plo[hh][kg][e] = l0;
+                    plo[hh][kg][e + 1] = l1;
+                  } else {
+                    round16x2(pa0, pa1, h0, h1);
+                  }
+                  phi[hh][kg][e] = h0;
+                  phi[hh][kg][e + 1] = h1;
+                  if constexpr (kSplit) {
+                    split16x2(pb0, pb1, h0, h1, l0, l1);
+                    plo[hh][kg][4 + e] = l0;
+                    plo[hh][kg][5 + e] = l1;
+                  } else {
+                    round16x2(pb0, pb1, h0, h1);
+                  }
+                  phi[hh][kg][4 + e] = h0;
+                  phi[hh][kg][5 + e] = h1;
+                }
+            };
+            // The tile's row sums: an all-ones A operand against P^T puts sum_k P[r][k]
+            // of the tile's keys in every entry of lane r's accumulator.
+            auto row_sum = [&]() {
+              f32x4 tl = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int kg = 0; kg < 2; ++kg) {
+                tl = M::mma(ones, phi[hh][kg], tl);
+                if constexpr (kSplit) tl = M::mma(ones, plo[hh][kg], tl);
+              }
+              return tl[0];
+            };
+            if constexpr (kSplit) {
+              // hi + lo operands: twice the weight registers, no room for a second
+              // formation; every tile takes the max.
+              raise();
+              weights();
+              lsum[hh] += row_sum();
+            } else {
+              const bool fresh = __builtin_amdgcn_ballot_w64(m[hh] == -INFINITY) != 0;
+              if (fresh) raise();
+              weights();
+              float tl = row_sum();
+              if (!fresh && __builtin_amdgcn_ballot_w64(!(tl <= kSumMax)) != 0) {
+                raise();
+                weights();
+                tl = row_sum();
+              }
+              lsum[hh] += tl;
             }
           }
           // O^T += V^T P^T. Lane L reads tile row 32kg + 4g + L/4 (and +16), dims
@@ -455,7 +495,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
 #pragma unroll
           for (int mt = 0; mt < 4; ++mt)
             *reinterpret_cast<f32x4*>(xo + ((wave * 4 + mt) * 64 + lane) * 4) = o[0][mt];
-          *reinterpret_cast<float2*>(xml + (wave * 64 + lane) * 2) = make_float2(m[0], lacc[0][0]);
+          *reinterpret_cast<float2*>(xml + (wave * 64 + lane) * 2) = make_float2(m[0], lsum[0]);
         }
         __syncthreads();
         if (team == 0) {
@@ -463,7 +503,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
           const float m_new = fmaxf(m[0], ml.x);
           const float c0 = m[0] == -INFINITY ? 0.0f : exp2_weight(m[0] - m_new);
           const float c1 = ml.x == -INFINITY ? 0.0f : exp2_weight(ml.x - m_new);
-          lacc[0][0] = lacc[0][0] * c0 + ml.y * c1;
+          lsum[0] = lsum[0] * c0 + ml.y * c1;
 #pragma unroll
           for (int mt = 0; mt < 4; ++mt) {
             const f32x4 o1 = *reinterpret_cast<const f32x4*>(xo + ((wave * 4 + mt) * 64 + lane) * 4);
@@ -479,7 +519,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
 #pragma unroll
       for (int hh = 0; hh < kHeadsPerWave; ++hh) {
         if (hh >= nh) break;
-        const float il = 1.0f / lacc[hh][0];
+        const float il = 1.0f / lsum[hh];
         float* dst = out + (size_t(t) * n_heads + h0 + hh) * 64 + 4 * g;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<f32x4*>(dst + 16 * mt) = o[hh][mt] * il;
