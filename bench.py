@@ -699,11 +699,23 @@ def bench_mixed(args, torch, ie, O):
     ws = ie.attention_workspace(n_dec, NH, HD, nc)
     stream = torch.cuda.current_stream()
 
-    def prefill(i):
+    # The prompt as the engine's prompt step runs it (KvEngine::run): K/V appended, q
+    # rotated inside the prefill kernel (ie_hip_rope_cache_attention_prefill), where the
+    # library offers that; else the two calls (append rotating q in place, then prefill).
+    pf_fused = ie.rope_cache_attention_prefill_supported(KV_CODES[kv], NH, NKV, HD)
+
+    def prefill_two_calls(i):
         ie.rope_and_cache(pq, pk, pv, k_pool, v_pool, table, p_pos, p_seq, d_tab, max_pages,
                           NH, NKV, HD)
         ie.attention_prefill(p_out, pq, k_pool, v_pool, p_pos, p_seq, d_tab, max_pages, NH, NKV,
                              HD)
+
+    def prefill(i):
+        if not pf_fused:
+            prefill_two_calls(i)
+            return
+        ie.rope_cache_attention_prefill(p_out, pq, pk, pv, k_pool, v_pool, table, p_pos, p_seq,
+                                        d_tab, max_pages, NH, NKV, HD)
 
     def prefill_attn(i):
         ie.attention_prefill(p_out, pq, k_pool, v_pool, p_pos, p_seq, d_tab, max_pages, NH, NKV,
@@ -759,6 +771,9 @@ def bench_mixed(args, torch, ie, O):
     ms = time_steps(torch, step_serial, args.steps, args.warmup, stream)
     ms_pf = time_steps(torch, prefill_attn, args.steps, args.warmup, stream)
     ms_dec = time_steps(torch, decode, args.steps, args.warmup, stream)
+    ms_pfp = time_steps(torch, prefill, args.steps, args.warmup, stream)
+    ms_pfp2 = (time_steps(torch, prefill_two_calls, args.steps, args.warmup, stream) if pf_fused
+               else ms_pfp)
     ms_dec2 = time_steps(torch, decode_two_calls, args.steps, args.warmup, stream) if fused else ms_dec
     flops = 4 * NH * HD * P * (P + 1) // 2
     # Dense matrix peak of the type the prefill tiles run in: the 16-bit MFMA for
@@ -775,12 +790,17 @@ def bench_mixed(args, torch, ie, O):
         "config": {"workload": "config 5: 48 decode rows (L~U[256,2048]) + one 4,000-token "
                                "prefill into fresh pages after 25% page churn, one layer",
                    "kv_dtype": kv, "chunk_tokens": ct, "seed": args.seed},
-        "step": "one stream: the prefill, then the decode rows (the engine's order)",
+        "step": "one stream: the prompt's append + prefill, then the decode rows (the engine's "
+                "order and calls)",
         "ms_per_step_two_branches": round(ms_branches, 5),
         "two_branches_note": "a kernel-composition bound, not an engine path: the decode "
                              "half on a parallel graph branch beside the prefill",
         "prefill_attention_ms": round(ms_pf, 5),
         "prefill_tflops": round(tflops, 2),
+        "prefill_part_ms": round(ms_pfp, 5),
+        "prefill_part_calls": ("rope_cache_attention_prefill (the engine's prompt step)" if pf_fused
+                               else "rope_and_cache + attention_prefill"),
+        "prefill_part_two_calls_ms": round(ms_pfp2, 5),
         "decode_part_ms": round(ms_dec, 5),
         "decode_part_gbs": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 2),
         "decode_part_calls": ("rope_cache_attention_planned (the engine's decode step)" if fused
@@ -978,6 +998,8 @@ def extra_targets(args, torch, ie, O):
             "us_per_launch": mix["roofline"]["us_per_launch"],
             "tflops": mix["roofline"]["achieved"], "frac": mix["roofline"]["frac"],
             "mixed_step_ms": mix["ms_per_step"],
+            "prefill_part_ms": mix["prefill_part_ms"],
+            "prefill_part_two_calls_ms": mix["prefill_part_two_calls_ms"],
             "mixed_step_two_branches_ms": mix["ms_per_step_two_branches"],
             "decode_part_gbs": mix["decode_part_gbs"],
             "kernel": mix["roofline"]["kernel"]},

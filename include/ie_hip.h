@@ -255,6 +255,26 @@ int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, con
                              ie_kv_layout kv, int n_heads, int n_kv_heads, int head_dim,
                              hipStream_t stream);
 
+/* ie_hip_rope_and_cache followed by ie_hip_attention_prefill for a prompt
+ * chunk: the reference's per-layer prompt sequence rope_and_cache +
+ * attention_prefill (src/cuda/kernels.cuh:69-74,89-96, called at
+ * src/cuda/cuda_runner.cu:440-445), with the rotation of q folded into the
+ * prefill kernel: K and V are rotated (K) and stored by the append as there, q
+ * is only read and rotated in registers as the prefill kernel loads it (the
+ * same arithmetic, so pages and `out` are bit-identical to the two calls; q in
+ * memory stays unrotated, and the append skips q's 2 x 3.5 KB per row). Rows
+ * as for attention_prefill (consecutive positions of one sequence); the matrix-
+ * core prefill kernels only (f32, f16, bf16 caches; head_dim 64, at most 8
+ * query heads per KV head; not under IE_HIP_IMPL_VALU), else EINVAL: use the two
+ * calls. The table must be 16-byte aligned device memory. */
+int ie_hip_rope_cache_attention_prefill_supported(int kv_dtype, int n_heads, int n_kv_heads,
+                                                   int head_dim);
+int ie_hip_rope_cache_attention_prefill(float* out, const float* q, const float* k, const float* v,
+                                        void* k_pool, void* v_pool, const float* rope_table,
+                                        int table_positions, int T, const int32_t* row_pos,
+                                        const int32_t* row_seq, ie_kv_layout kv, int n_heads,
+                                        int n_kv_heads, int head_dim, hipStream_t stream);
+
 /* ------------------------------------------------------------- gathers ---
  * dst[r, :] = src[rows[r], :] for r < R. Replaces gather_rows
  * (src/cuda/kernels.cuh:101-102, kernels.cu:778-783,1422-1425). */

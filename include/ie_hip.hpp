@@ -123,6 +123,24 @@ inline void attention_prefill(float* out, const float* q, const void* k_pool, co
                                  n_kv_heads, head_dim, stream));
 }
 
+/* rope_and_cache followed by attention_prefill for a prompt chunk, q rotated
+ * inside the prefill kernel (see ie_hip_rope_cache_attention_prefill). */
+inline bool rope_cache_attention_prefill_supported(int kv_dtype, int n_heads, int n_kv_heads,
+                                                   int head_dim) {
+  return ie_hip_rope_cache_attention_prefill_supported(kv_dtype, n_heads, n_kv_heads,
+                                                       head_dim) != 0;
+}
+inline void rope_cache_attention_prefill(float* out, const float* q, const float* k,
+                                         const float* v, void* k_pool, void* v_pool,
+                                         const float* rope_table, int table_positions, int T,
+                                         const int* row_pos, const int* row_seq,
+                                         const KvLayout& kv, int n_heads, int n_kv_heads,
+                                         int head_dim, hipStream_t stream) {
+  check(ie_hip_rope_cache_attention_prefill(out, q, k, v, k_pool, v_pool, rope_table,
+                                            table_positions, T, row_pos, row_seq, kv.c(), n_heads,
+                                            n_kv_heads, head_dim, stream));
+}
+
 /* attention_chunks (kernels.cuh:98-99), for a given partition length. */
 inline int attention_chunks(int context_tokens, int chunk_tokens) {
   const int n = ie_hip_attention_chunks(context_tokens, chunk_tokens);

@@ -91,7 +91,8 @@ struct StepInfo {
   int rows = 0, logit_rows = 0;
   bool graph = false;   // replayed a decode graph
   bool prompt = false;  // prefill attention (rows: consecutive positions of one sequence)
-  bool fused = false;   // RoPE + append + attention in one launch per layer
+  bool fused = false;   // decode: RoPE + append + attention in one launch per layer;
+                        // prompt: q rotated inside the prefill kernel (append of K/V only)
   bool planned = false; // flash-decoding read a host-built work list (ie_hip_attention_plan)
   int chunk_tokens = 0, chunks = 0;  // flash-decoding partition (0 for a prompt)
 };
@@ -318,7 +319,10 @@ class KvEngine {
                attention_prefill_supported(cfg_.num_heads, cfg_.num_kv_heads, cfg_.head_dim);
     for (int t = 1; s.prompt && t < T; ++t)
       s.prompt = seq[t] == seq[0] && pos[t] == pos[0] + t;
-    if (!s.prompt) {
+    if (s.prompt) {
+      s.fused = rope_cache_attention_prefill_supported(kv_dtype_, cfg_.num_heads,
+                                                       cfg_.num_kv_heads, cfg_.head_dim);
+    } else {
       s.chunk_tokens = chunk_tokens_;
       // A recorded graph covers any position a sequence can reach; a direct
       // step only the context it has (the count does not change the sums).
@@ -481,7 +485,10 @@ class KvEngine {
       void* kp = k_pool(l);
       void* vp = v_pool(l);
       const int32_t* plan = inputs_ + plan_offset(T, s.logit_rows);
-      if (s.fused && s.planned) {
+      if (s.prompt && s.fused) {
+        rope_cache_attention_prefill(attn_, q_, k_, v_, kp, vp, rope_, lim_.max_seq_len, T, rpos,
+                                     rseq, kv, NH, NKV, HD, stream_);
+      } else if (s.fused && s.planned) {
         rope_cache_attention_planned(attn_, q_, k_, v_, kp, vp, rope_, lim_.max_seq_len, T, rpos,
                                      rseq, kv, s.chunks, s.chunk_tokens, workspace_, plan,
                                      plan_ints_, NH, NKV, HD, stream_);

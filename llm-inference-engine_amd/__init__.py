@@ -81,6 +81,9 @@ _SIGS = {
                                          KvLayout, _i, _i, _vp, _i, _i, _i, _vp]),
     "ie_hip_attention_prefill_supported": (_i, [_i, _i, _i]),
     "ie_hip_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, KvLayout, _i, _i, _i, _vp]),
+    "ie_hip_rope_cache_attention_prefill_supported": (_i, [_i, _i, _i, _i]),
+    "ie_hip_rope_cache_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp,
+                                                 _vp, KvLayout, _i, _i, _i, _vp]),
     "ie_hip_gather_rows": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "ie_hip_gather_kv": (_i, [_vp, _vp, KvLayout, _i, _i, _i, _vp]),
     "ie_hip_argmax_rows": (_i, [_vp, _vp, _i, _i, _vp]),
@@ -313,6 +316,27 @@ def rope_cache_attention(out, q, k, v, k_pool, v_pool, table, row_pos, row_seq, 
                                              _ptr(row_pos), _ptr(row_seq), kv, num_chunks,
                                              chunk_tokens, _ptr(workspace), n_heads, n_kv_heads,
                                              head_dim, _stream(stream)))
+
+
+def rope_cache_attention_prefill_supported(kv_dtype: int, n_heads: int, n_kv_heads: int,
+                                           head_dim: int) -> bool:
+    return bool(lib().ie_hip_rope_cache_attention_prefill_supported(kv_dtype, n_heads, n_kv_heads,
+                                                                    head_dim))
+
+
+def rope_cache_attention_prefill(out, q, k, v, k_pool, v_pool, table, row_pos, row_seq, tables,
+                                 max_pages: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                                 stream=None) -> None:
+    """rope_and_cache + attention_prefill of one prompt chunk, q rotated inside the prefill
+    kernel (q is not modified)."""
+    T = row_pos.numel()
+    kv = layout(tables, max_pages, k_pool.numel() // (PAGE_SIZE * n_kv_heads * head_dim),
+                _dtype_code(k_pool))
+    _check(lib().ie_hip_rope_cache_attention_prefill(_ptr(out), _ptr(q), _ptr(k), _ptr(v),
+                                                     _ptr(k_pool), _ptr(v_pool), _ptr(table),
+                                                     table.shape[0], T, _ptr(row_pos),
+                                                     _ptr(row_seq), kv, n_heads, n_kv_heads,
+                                                     head_dim, _stream(stream)))
 
 
 def attention_prefill_supported(n_heads: int, n_kv_heads: int, head_dim: int) -> bool:

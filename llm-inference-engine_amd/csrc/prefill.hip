@@ -219,11 +219,44 @@ int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, con
   if (impl != IE_HIP_IMPL_VALU &&
       prefill_mfma_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim))
     return prefill_mfma_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads,
-                               n_kv_heads, stream);
+                               n_kv_heads, PrefillRope{}, stream);
   if (impl == IE_HIP_IMPL_MFMA)
     return fail(IE_HIP_EINVAL, "attention_prefill: the MFMA kernels do not support this shape");
   return prefill_valu_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads, n_kv_heads,
                              stream);
+}
+
+int ie_hip_rope_cache_attention_prefill_supported(int kv_dtype, int n_heads, int n_kv_heads,
+                                                   int head_dim) {
+  return attention_impl() != IE_HIP_IMPL_VALU &&
+         prefill_mfma_supported(kv_dtype, n_heads, n_kv_heads, head_dim);
+}
+
+int ie_hip_rope_cache_attention_prefill(float* out, const float* q, const float* k, const float* v,
+                                        void* k_pool, void* v_pool, const float* rope_table,
+                                        int table_positions, int T, const int32_t* row_pos,
+                                        const int32_t* row_seq, ie_kv_layout kv, int n_heads,
+                                        int n_kv_heads, int head_dim, hipStream_t stream) {
+  clear_error();
+  if (int rc = check_layout(kv, "rope_cache_attention_prefill")) return rc;
+  if (!ie_hip_rope_cache_attention_prefill_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim))
+    return fail(IE_HIP_EINVAL,
+                "rope_cache_attention_prefill: needs the matrix-core prefill kernels (head_dim 64, "
+                "at most 8 query heads per KV head, not IE_HIP_IMPL_VALU); use rope_and_cache + "
+                "attention_prefill");
+  if (T < 0) return fail(IE_HIP_EINVAL, "rope_cache_attention_prefill: negative row count");
+  if (T == 0) return IE_HIP_OK;
+  if (!out || !q || !k || !v || !k_pool || !v_pool || !rope_table || !row_pos || !row_seq)
+    return fail(IE_HIP_EINVAL, "rope_cache_attention_prefill: null pointer");
+  if (table_positions <= 0)
+    return fail(IE_HIP_EINVAL, "rope_cache_attention_prefill: empty RoPE table");
+  // K and V rotated (K) and stored; q is left as it is and rotated by the prefill
+  // kernel as it loads it.
+  if (int rc = ie_hip_rope_and_cache(nullptr, k, v, k_pool, v_pool, rope_table, table_positions, T,
+                                     row_pos, row_seq, kv, n_heads, n_kv_heads, head_dim, stream))
+    return rc;
+  return prefill_mfma_launch(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, n_heads, n_kv_heads,
+                             PrefillRope{rope_table, table_positions}, stream);
 }
 
 }  // extern "C"

@@ -82,7 +82,8 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
                     const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
                     int T, const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
                     const int32_t* __restrict__ tables, int max_pages, int num_pages, int n_heads,
-                    int n_kv_heads, int n_blocks) {
+                    int n_kv_heads, int n_blocks, const float* __restrict__ rope,
+                    int rope_positions) {
   using M = Mfma<KV>;
   using op = typename M::op;
   using E = typename M::elem;
@@ -120,6 +121,9 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   // in-pool bits of team tm's tile, bit 8 = some tile of the step needs V rows
   // zeroed (past max_pos or a page outside the pool). One LDS read per step.
   int* const step_flags = ids + 4 * (kSegTiles + kTeams);
+  // With a RoPE table: the cos/sin rows of the block's 16 positions, staged once
+  // per block ([16][64] f32 after the step flags) and read by every wave.
+  float* const rope_rows = reinterpret_cast<float*>(step_flags + kSegTiles);
   int seg0 = 0;  // first tile of the segment in progress
   auto tile_ids = [&](const int tile) {
     return *reinterpret_cast<const int4*>(ids + 4 * (tile - seg0));
@@ -189,44 +193,89 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     const int n_tiles = max_pos / kKeys + 1;
 
     // Queries of row t0 + r for the wave's heads, times log2(e)/8 (split hi + lo
-    // for bf16): the B operands of S^T (dims 32 ks + 8g .. +8).
+    // for bf16): the B operands of S^T (dims 32 ks + 8g .. +8). Their loads (and
+    // the RoPE table rows') are issued here and turned into operands (make_q) only
+    // after the block's first page-id staging is under way, so that the query's
+    // round trip and the table's overlap instead of following each other.
     const int t = t0 + r;
     const bool row_ok = t < T;
     const int rp = pos0 + t;  // this lane's row position
-    op qhi[kHeadsPerWave][2], qlo[kHeadsPerWave][2];
+    float4 qa[kHeadsPerWave][2][2];
 #pragma unroll
-    for (int hh = 0; hh < kHeadsPerWave; ++hh) {
-      float4 a[2][2];
+    for (int hh = 0; hh < kHeadsPerWave; ++hh)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        a[ks][0] = a[ks][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        qa[hh][ks][0] = qa[hh][ks][1] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (row_ok && hh < nh) {
           const float4* src = reinterpret_cast<const float4*>(
               q + (size_t(t) * n_heads + h0 + hh) * 64 + 32 * ks + 8 * g);
-          a[ks][0] = src[0];
-          a[ks][1] = src[1];
+          qa[hh][ks][0] = src[0];
+          qa[hh][ks][1] = src[1];
         }
       }
-      const float qs = 0.125f * kLog2e;
+    // With a RoPE table (ie_hip_rope_cache_attention_prefill) q arrives unrotated,
+    // and the rotation ie_hip_rope_and_cache would have applied in place happens
+    // in make_q: lane (g, r) holds dims 8g + j and 32 + 8g + j, the rotation
+    // pairs, and takes cos/sin of its row's position from the table; the same
+    // fmaf in the same order, so the same float32 values. Rows whose position
+    // lies outside the table are used unrotated, as there. The table is read for
+    // every lane (row 0's entries where the row is not rotated), the rotation
+    // applied by selection.
+    const bool rot = rope && row_ok && rp >= 0 && rp < rope_positions;
+    op qhi[kHeadsPerWave][2], qlo[kHeadsPerWave][2];
+    auto make_q = [&]() {
+      float4 tcs[4] = {};  // cos of dims 8g .. 8g+7, then sin (rows staged in LDS)
+      if (rope) {
+        const float* trow = rope_rows + r * 64 + 8 * g;
+        tcs[0] = *reinterpret_cast<const float4*>(trow);
+        tcs[1] = *reinterpret_cast<const float4*>(trow + 4);
+        tcs[2] = *reinterpret_cast<const float4*>(trow + 32);
+        tcs[3] = *reinterpret_cast<const float4*>(trow + 36);
+      }
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const float x[8] = {a[ks][0].x, a[ks][0].y, a[ks][0].z, a[ks][0].w,
-                            a[ks][1].x, a[ks][1].y, a[ks][1].z, a[ks][1].w};
+      for (int hh = 0; hh < kHeadsPerWave; ++hh) {
+        float x[2][8] = {{qa[hh][0][0].x, qa[hh][0][0].y, qa[hh][0][0].z, qa[hh][0][0].w,
+                          qa[hh][0][1].x, qa[hh][0][1].y, qa[hh][0][1].z, qa[hh][0][1].w},
+                         {qa[hh][1][0].x, qa[hh][1][0].y, qa[hh][1][0].z, qa[hh][1][0].w,
+                          qa[hh][1][1].x, qa[hh][1][1].y, qa[hh][1][1].z, qa[hh][1][1].w}};
+        if (rope) {
+          const float cs[8] = {tcs[0].x, tcs[0].y, tcs[0].z, tcs[0].w,
+                               tcs[1].x, tcs[1].y, tcs[1].z, tcs[1].w};
+          const float sn[8] = {tcs[2].x, tcs[2].y, tcs[2].z, tcs[2].w,
+                               tcs[3].x, tcs[3].y, tcs[3].z, tcs[3].w};
+          const bool on = rot && hh < nh;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          E hv, lv = static_cast<E>(0.0f);
-          if constexpr (kSplit)
-            split16(x[j] * qs, hv, lv);
-          else
-            hv = static_cast<E>(x[j] * qs);
-          qhi[hh][ks][j] = hv;
-          qlo[hh][ks][j] = lv;
+          for (int j = 0; j < 8; ++j) {
+            const float x0 = x[0][j], x1 = x[1][j];
+            const float r0 = __builtin_fmaf(x0, cs[j], -(x1 * sn[j]));  // x0*c - x1*s
+            const float r1 = __builtin_fmaf(x1, cs[j], x0 * sn[j]);     // x1*c + x0*s
+            x[0][j] = on ? r0 : x0;
+            x[1][j] = on ? r1 : x1;
+          }
+        }
+        const float qs = 0.125f * kLog2e;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            E hv, lv = static_cast<E>(0.0f);
+            if constexpr (kSplit) {
+              split16(x[ks][j] * qs, hv, lv);
+            } else {
+              // The float32 product, then its f16 rounding: kept opaque so that no
+              // instantiation folds the two into one mixed-precision fma (a single
+              // rounding of the exact product), whether q was rotated here or not.
+              float xq = x[ks][j] * qs;
+              asm("" : "+v"(xq));
+              hv = static_cast<E>(xq);
+            }
+            qhi[hh][ks][j] = hv;
+            qlo[hh][ks][j] = lv;
+          }
         }
       }
-    }
+    };
 
-    // Per head: running max (base 2), the row's sum of weights, and O^T
-    // (lane (g, r) holds row r, dims 16 mt + 4g + e).
     // nref: every entry -(the reference max, 0 while m = -inf), the value the S
     // accumulators start from; kept across steps and changed only when m is raised.
     float m[kHeadsPerWave];
@@ -249,14 +298,25 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     // last tile still loads (page 0 or in-pool pages, never read), keeping every
     // step's load count the same for the counted waits. Segments hold an even
     // number of tiles, so a step never straddles two.
-    for (seg0 = 0; seg0 < n_tiles; seg0 += kSegTiles) {
-      const int n_steps = (min(kSegTiles, n_tiles - seg0) + kTeams - 1) / kTeams;
+    // Staging of the segment starting at seg0: its page ids and step flags into
+    // LDS, and the ring's first steps issued.
+    int n_steps = 0;
+    auto stage = [&]() {
+      n_steps = (min(kSegTiles, n_tiles - seg0) + kTeams - 1) / kTeams;
       // The ring is idle here and every wave is past its last read of the previous
       // segment's ids (the last step, or the team exchange, ended in a barrier).
       for (int i = tid; i < 4 * kTeams * n_steps; i += 64 * kWaves * kTeams) {
         const int pi = 4 * seg0 + i;
         const int id = pi < max_pages ? tab[pi] : -1;
         ids[i] = id >= 0 && id < num_pages ? id : -1;
+      }
+      // The block's RoPE rows (first segment only; rows outside the table or past
+      // the block's rows are not used and stay as they are).
+      if (rope && seg0 == 0 && tid < kRows * 16) {
+        const int ri = tid >> 4, p = pos0 + t0 + ri;
+        if (t0 + ri < T && p >= 0 && p < rope_positions)
+          reinterpret_cast<float4*>(rope_rows)[tid] =
+              reinterpret_cast<const float4*>(rope + size_t(p) * 64)[tid & 15];
       }
       __syncthreads();
       for (int i = tid; i < n_steps; i += 64 * kWaves * kTeams) {
@@ -274,6 +334,11 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       }  // read after the barrier below
       for (int pre = 0; pre < kRingSteps - 1 && pre < n_steps; ++pre)
         issue(buffer(pre, team), seg0 + kTeams * pre + team);
+    };
+    seg0 = 0;
+    stage();
+    make_q();  // the query's loads landed with the staging's
+    for (;;) {
       wait_steps(min(kRingSteps - 2, n_steps - 1));  // step 0 has landed
       __syncthreads();
 
@@ -481,6 +546,9 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
         wait_steps(max(0, min(kRingSteps - 2, n_steps - st - 2)));
         __syncthreads();
       }
+      seg0 += kSegTiles;
+      if (seg0 >= n_tiles) break;
+      stage();
     }
 
     // Teams 1.. hand their (m, l, O) to team 0 through LDS (the ring is idle:
@@ -533,16 +601,18 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
 template <int kTeams>
 constexpr int prefill_lds_bytes() {
   return (kTeams == 1 ? 4 : 3) * kTeams * kBufBytes + 16 * (kSegTiles + kTeams) +
-         4 * kSegTiles;
+         4 * kSegTiles + kRows * 64 * 4;
 }
 
 template <int KV, int W, int kTeams, bool kSplitF16>
 int launch_prefill_split(const dim3 grid, float* out, const float* q, const uint16_t* kp,
                          const uint16_t* vp, int T, const int32_t* row_pos,
                          const int32_t* row_seq, const ie_kv_layout& kv, int n_heads,
-                         int n_kv_heads, int n_blocks, hipStream_t stream) {
+                         int n_kv_heads, int n_blocks, const PrefillRope& rope,
+                         hipStream_t stream) {
   constexpr int lds = prefill_lds_bytes<kTeams>();
-  static_assert(lds - 16 * (kSegTiles + kTeams) - 4 * kSegTiles >= W * 4096 + W * 512,
+  static_assert(lds - 16 * (kSegTiles + kTeams) - 4 * kSegTiles - kRows * 64 * 4 >=
+                    W * 4096 + W * 512,
                 "team exchange area must fit in the ring");
   if (lds > 65536) {  // above the default dynamic-LDS cap, within gfx950's 160 KB
     static const hipError_t attr = hipFuncSetAttribute(
@@ -552,7 +622,8 @@ int launch_prefill_split(const dim3 grid, float* out, const float* q, const uint
   }
   hipLaunchKernelGGL((prefill_mfma_kernel<KV, W, kTeams, kSplitF16>), grid,
                      dim3(64 * W * kTeams), lds, stream, out, q, kp, vp, T, row_pos, row_seq,
-                     kv.tables, kv.max_pages, kv.num_pages, n_heads, n_kv_heads, n_blocks);
+                     kv.tables, kv.max_pages, kv.num_pages, n_heads, n_kv_heads, n_blocks,
+                     rope.table, rope.positions);
   return check_launch("attention_prefill_mfma");
 }
 
@@ -562,18 +633,21 @@ template <int KV, int W, int kTeams>
 int launch_prefill_variant(const dim3 grid, float* out, const float* q, const uint16_t* kp,
                            const uint16_t* vp, int T, const int32_t* row_pos,
                            const int32_t* row_seq, const ie_kv_layout& kv, int n_heads,
-                           int n_kv_heads, int n_blocks, hipStream_t stream) {
+                           int n_kv_heads, int n_blocks, const PrefillRope& rope,
+                           hipStream_t stream) {
   if (KV == IE_KV_F16 && prefill_rounding() == IE_HIP_PREFILL_SPLIT)
     return launch_prefill_split<KV, W, kTeams, true>(grid, out, q, kp, vp, T, row_pos, row_seq,
-                                                     kv, n_heads, n_kv_heads, n_blocks, stream);
+                                                     kv, n_heads, n_kv_heads, n_blocks, rope,
+                                                     stream);
   return launch_prefill_split<KV, W, kTeams, false>(grid, out, q, kp, vp, T, row_pos, row_seq,
-                                                    kv, n_heads, n_kv_heads, n_blocks, stream);
+                                                    kv, n_heads, n_kv_heads, n_blocks, rope,
+                                                    stream);
 }
 
 template <int KV>
 int launch_prefill_mfma(float* out, const float* q, const uint16_t* kp, const uint16_t* vp, int T,
                         const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
-                        int n_heads, int n_kv_heads, hipStream_t stream) {
+                        int n_heads, int n_kv_heads, const PrefillRope& rope, hipStream_t stream) {
   const int group = n_heads / n_kv_heads;
   const int waves = (group + kHeadsPerWave - 1) / kHeadsPerWave;
   const int n_blocks = (T + kRows - 1) / kRows;
@@ -585,9 +659,11 @@ int launch_prefill_mfma(float* out, const float* q, const uint16_t* kp, const ui
 #define IE_PF_CASE(W)                                                                             \
   case W:                                                                                         \
     return teams2 ? launch_prefill_variant<KV, W, 2>(grid, out, q, kp, vp, T, row_pos, row_seq,   \
-                                                      kv, n_heads, n_kv_heads, n_blocks, stream)  \
+                                                      kv, n_heads, n_kv_heads, n_blocks, rope,    \
+                                                      stream)                                     \
                   : launch_prefill_variant<KV, W, 1>(grid, out, q, kp, vp, T, row_pos, row_seq,   \
-                                                      kv, n_heads, n_kv_heads, n_blocks, stream);
+                                                      kv, n_heads, n_kv_heads, n_blocks, rope,    \
+                                                      stream);
   switch (waves) {
     IE_PF_CASE(1)
     IE_PF_CASE(2)
@@ -631,7 +707,8 @@ prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
                         const float* __restrict__ k_pool, const float* __restrict__ v_pool, int T,
                         const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
                         const int32_t* __restrict__ tables, int max_pages, int num_pages,
-                        int n_heads, int n_kv_heads, int n_blocks) {
+                        int n_heads, int n_kv_heads, int n_blocks,
+                        const float* __restrict__ rope, int rope_positions) {
   // A tile's 32 loads of 1 KB (16 K, 16 V), spread evenly over kDmaWaves waves.
   constexpr int kDmaWaves = kWaves >= 4 ? 4 : kWaves >= 2 ? 2 : 1;
   constexpr int kPerWave = 32 / kDmaWaves;
@@ -712,17 +789,42 @@ prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
     // Row r's query, times log2(e)/8, at dims 16g .. 16g+15 (B of the score steps).
     float qb[16];
     {
-      const float4* src = reinterpret_cast<const float4*>(
-          q + (size_t(row_ok ? t : t0) * n_heads + h0) * 64 + 16 * g);
+      const float* qrow = q + (size_t(row_ok ? t : t0) * n_heads + h0) * 64;
       const float qs = row_ok ? 0.125f * kLog2e : 0.0f;
+      float x[16];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float4 x = src[i];
-        qb[4 * i + 0] = x.x * qs;
-        qb[4 * i + 1] = x.y * qs;
-        qb[4 * i + 2] = x.z * qs;
-        qb[4 * i + 3] = x.w * qs;
+        const float4 v = reinterpret_cast<const float4*>(qrow + 16 * g)[i];
+        x[4 * i + 0] = v.x;
+        x[4 * i + 1] = v.y;
+        x[4 * i + 2] = v.z;
+        x[4 * i + 3] = v.w;
       }
+      // With a RoPE table, q arrives unrotated and is rotated here as
+      // ie_hip_rope_and_cache would have (the same fmaf, the same float32
+      // values). Dim d = 16g + j pairs with d + 32 (g < 2, this lane holds x0)
+      // or d - 32 (g >= 2, x1): the partner's 16 dims are read as well.
+      if (rope && row_ok && rp >= 0 && rp < rope_positions) {
+        const int i0 = 16 * (g & 1);  // rotation index of dim 16g
+        const float* trow = rope + size_t(rp) * 64 + i0;
+        const float* prow = qrow + 16 * (g ^ 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 pv = reinterpret_cast<const float4*>(prow)[i];
+          const float4 c4 = reinterpret_cast<const float4*>(trow)[i];
+          const float4 s4 = reinterpret_cast<const float4*>(trow + 32)[i];
+          const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
+          const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float own = x[4 * i + e], other = pp[e];
+            x[4 * i + e] = g < 2 ? __builtin_fmaf(own, cc[e], -(other * ss[e]))  // x0*c - x1*s
+                                 : __builtin_fmaf(own, cc[e], other * ss[e]);    // x1*c + x0*s
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) qb[i] = x[i] * qs;
     }
     float m = -INFINITY, l = 0.0f;  // running max (base 2), this lane's part of the sum
     f32x4 o[4];                      // o[mt][t]: row r, dim 16g + 4t + mt
@@ -860,7 +962,7 @@ template <int W>
 int launch_prefill_f32(const dim3 grid, float* out, const float* q, const float* kp,
                        const float* vp, int T, const int32_t* row_pos, const int32_t* row_seq,
                        const ie_kv_layout& kv, int n_heads, int n_kv_heads, int n_blocks,
-                       hipStream_t stream) {
+                       const PrefillRope& rope, hipStream_t stream) {
   constexpr int lds = kRingF32 * kBufF32 + 16 * kSegTiles;  // 96 KB ring + the segment's page ids
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(prefill_mfma_f32_kernel<W>),
@@ -868,7 +970,7 @@ int launch_prefill_f32(const dim3 grid, float* out, const float* q, const float*
   if (int rc = check_hip(attr, "hipFuncSetAttribute(attention_prefill_mfma_f32)")) return rc;
   hipLaunchKernelGGL((prefill_mfma_f32_kernel<W>), grid, dim3(64 * W), lds, stream, out, q, kp,
                      vp, T, row_pos, row_seq, kv.tables, kv.max_pages, kv.num_pages, n_heads,
-                     n_kv_heads, n_blocks);
+                     n_kv_heads, n_blocks, rope.table, rope.positions);
   return check_launch("attention_prefill_mfma_f32");
 }
 
@@ -882,7 +984,10 @@ bool prefill_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_
 
 int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                         const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
-                        int n_heads, int n_kv_heads, hipStream_t stream) {
+                        int n_heads, int n_kv_heads, const PrefillRope& rope,
+                        hipStream_t stream) {
+  if (rope.table && (reinterpret_cast<uintptr_t>(rope.table) & 15))
+    return fail(IE_HIP_EINVAL, "attention_prefill: the RoPE table must be 16-byte aligned");
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) & 15)
     return fail(IE_HIP_EINVAL, "attention_prefill: q, out and the pools must be 16-byte aligned");
@@ -896,7 +1001,7 @@ int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const vo
 #define IE_PF32_CASE(W)                                                                      \
   case W:                                                                                    \
     return launch_prefill_f32<W>(grid, out, q, kf, vf, T, row_pos, row_seq, kv, n_heads,     \
-                                 n_kv_heads, n_blocks, stream);
+                                 n_kv_heads, n_blocks, rope, stream);
       IE_PF32_CASE(1)
       IE_PF32_CASE(2)
       IE_PF32_CASE(3)
@@ -913,9 +1018,9 @@ int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const vo
   const uint16_t* vp = static_cast<const uint16_t*>(v_pool);
   if (kv.kv_dtype == IE_KV_F16)
     return launch_prefill_mfma<IE_KV_F16>(out, q, kp, vp, T, row_pos, row_seq, kv, n_heads,
-                                          n_kv_heads, stream);
+                                          n_kv_heads, rope, stream);
   return launch_prefill_mfma<IE_KV_BF16>(out, q, kp, vp, T, row_pos, row_seq, kv, n_heads,
-                                         n_kv_heads, stream);
+                                         n_kv_heads, rope, stream);
 }
 
 }  // namespace iehip
