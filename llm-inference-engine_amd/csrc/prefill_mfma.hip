@@ -71,6 +71,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyMax = 8.0f;           // log2 headroom of the lazily raised softmax max
 constexpr float kSumMax = 16384.0f;        // largest tile row sum taken without a new max
 constexpr int kSegTiles = 512;             // key tiles (32,768 keys) with page ids in LDS at once
+constexpr int kRopeStride = 68;            // floats per staged RoPE row (64 + 4 of padding)
 
 // kWaves = group / kHeadsPerWave waves per team (rounded up), wave w of a team
 // taking query heads kHeadsPerWave * w .. of the KV head. kTeams teams of
@@ -122,7 +123,9 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   // zeroed (past max_pos or a page outside the pool). One LDS read per step.
   int* const step_flags = ids + 4 * (kSegTiles + kTeams);
   // With a RoPE table: the cos/sin rows of the block's 16 positions, staged once
-  // per block ([16][64] f32 after the step flags) and read by every wave.
+  // per block after the step flags and read by every wave; rows kRopeStride
+  // floats apart (64 + 4), so that the 16 rows one lane group reads at the same
+  // offset fall into different banks.
   float* const rope_rows = reinterpret_cast<float*>(step_flags + kSegTiles);
   int seg0 = 0;  // first tile of the segment in progress
   auto tile_ids = [&](const int tile) {
@@ -226,7 +229,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
     auto make_q = [&]() {
       float4 tcs[4] = {};  // cos of dims 8g .. 8g+7, then sin (rows staged in LDS)
       if (rope) {
-        const float* trow = rope_rows + r * 64 + 8 * g;
+        const float* trow = rope_rows + r * kRopeStride + 8 * g;
         tcs[0] = *reinterpret_cast<const float4*>(trow);
         tcs[1] = *reinterpret_cast<const float4*>(trow + 4);
         tcs[2] = *reinterpret_cast<const float4*>(trow + 32);
@@ -315,7 +318,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
       if (rope && seg0 == 0 && tid < kRows * 16) {
         const int ri = tid >> 4, p = pos0 + t0 + ri;
         if (t0 + ri < T && p >= 0 && p < rope_positions)
-          reinterpret_cast<float4*>(rope_rows)[tid] =
+          reinterpret_cast<float4*>(rope_rows + ri * kRopeStride)[tid & 15] =
               reinterpret_cast<const float4*>(rope + size_t(p) * 64)[tid & 15];
       }
       __syncthreads();
@@ -601,7 +604,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
 template <int kTeams>
 constexpr int prefill_lds_bytes() {
   return (kTeams == 1 ? 4 : 3) * kTeams * kBufBytes + 16 * (kSegTiles + kTeams) +
-         4 * kSegTiles + kRows * 64 * 4;
+         4 * kSegTiles + kRows * kRopeStride * 4;
 }
 
 template <int KV, int W, int kTeams, bool kSplitF16>
@@ -611,7 +614,7 @@ int launch_prefill_split(const dim3 grid, float* out, const float* q, const uint
                          int n_kv_heads, int n_blocks, const PrefillRope& rope,
                          hipStream_t stream) {
   constexpr int lds = prefill_lds_bytes<kTeams>();
-  static_assert(lds - 16 * (kSegTiles + kTeams) - 4 * kSegTiles - kRows * 64 * 4 >=
+  static_assert(lds - 16 * (kSegTiles + kTeams) - 4 * kSegTiles - kRows * kRopeStride * 4 >=
                     W * 4096 + W * 512,
                 "team exchange area must fit in the ring");
   if (lds > 65536) {  // above the default dynamic-LDS cap, within gfx950's 160 KB
