@@ -193,9 +193,7 @@ class KvEngine {
     // work list the 16-bit kernel would otherwise locate on the device (row
     // positions -> the row's table -> K/V): built here from host data, it cuts
     // that chain to one load.
-    plan_ints_ = kv_dtype_ == IE_KV_F32
-                     ? 0
-                     : attention_plan_ints(attn_rows_, max_chunks_, chunk_tokens_);
+    plan_ints_ = attention_plan_ints(attn_rows_, max_chunks_, chunk_tokens_);
 
     pages_ = ie_pages_create(lim_.num_pages, lim_.max_batch, lim_.max_seq_len);
     if (!pages_) throw std::runtime_error(ie_hip_last_error());
@@ -566,7 +564,7 @@ class KvEngine {
   LayerBody body_;
   std::string name_;
   int chunk_tokens_ = 0, max_chunks_ = 0, attn_rows_ = 0, max_pages_per_seq_ = 0;
-  size_t plan_ints_ = 0;  // capacity of a step's work list (0: f32 caches, no plan)
+  size_t plan_ints_ = 0;  // capacity of a step's work list
 
   ie_page_pool* pages_ = nullptr;  // free list, sequences, host page table
   DeviceArena arena_;

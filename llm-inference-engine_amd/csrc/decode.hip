@@ -677,7 +677,7 @@ int attention_call(float* out, const float* q, const void* k_pool, const void* v
   if (impl != IE_HIP_IMPL_VALU &&
       decode_mfma_f32_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim, chunk_tokens))
     return decode_mfma_f32(out, q, k_pool, v_pool, T, row_pos, row_seq, kv, num_chunks,
-                           chunk_tokens, workspace, n_heads, n_kv_heads, stream);
+                           chunk_tokens, workspace, n_heads, n_kv_heads, stream, plan);
   if (impl == IE_HIP_IMPL_MFMA)
     return fail(IE_HIP_EINVAL, "attention: the MFMA kernels do not support this shape "
                                "(kv_dim 128, n_heads <= 16; 16-bit KV: chunk a multiple of 64 "

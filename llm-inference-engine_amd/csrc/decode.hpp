@@ -51,13 +51,14 @@ int decode_merge(float* out, const Workspace& ws, const int32_t* row_pos, int T,
 int attention_impl();
 
 // float32 KV on v_mfma_f32_16x16x4_f32 (KV rows of 128 elements, at most 16
-// query heads, chunks of whole pages up to 1024 tokens).
+// query heads, chunks of whole pages up to 1024 tokens); `plan`: a device copy of
+// ie_hip_attention_plan's work list, or nullptr.
 bool decode_mfma_f32_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim,
                                int chunk_tokens);
 int decode_mfma_f32(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                     const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
                     int num_chunks, int chunk_tokens, void* workspace, int n_heads,
-                    int n_kv_heads, hipStream_t stream);
+                    int n_kv_heads, hipStream_t stream, const int32_t* plan);
 bool decode_mfma_supported(int kv_dtype, int n_heads, int n_kv_heads, int head_dim,
                            int chunk_tokens);
 int decode_mfma(float* out, const float* q, const void* k_pool, const void* v_pool, int T,

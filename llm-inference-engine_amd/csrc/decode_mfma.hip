@@ -607,13 +607,37 @@ decode_partial_mfma_f32(float* __restrict__ out, float* __restrict__ part_o,
                         const float* __restrict__ k_pool, const float* __restrict__ v_pool,
                         const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
                         const int32_t* __restrict__ tables, int T, int max_pages, int num_pages,
-                        int n_heads, int group, int num_chunks, int chunk_tokens) {
+                        int n_heads, int group, int num_chunks, int chunk_tokens,
+                        const int32_t* __restrict__ plan) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x;
   const int g = lane >> 4, r = lane & 15;
+  // Which (row, chunk) this workgroup takes and the chunk's page ids, one per
+  // lane: from a host-built work list in one round trip (header, item and the
+  // lane's page id loaded together, as in the 16-bit kernel, with the same
+  // checks of the list against the launch), or located from row_pos and then
+  // read from the row's table (two dependent round trips).
   int t, c, p, seq;
-  if (!locate_chunk(blockIdx.x, T, row_pos, row_seq, num_chunks, chunk_tokens, lane, t, c, p, seq))
+  int pid_plan = -1;
+  if (plan) {
+    const int32_t* item = plan + kPlanHeader + size_t(blockIdx.x) * plan_stride(chunk_tokens);
+    pid_plan = lane < chunk_tokens / IE_HIP_PAGE_SIZE ? item[4 + lane] : -1;
+    const int4 head = *reinterpret_cast<const int4*>(plan);  // [items, chunk, chunks, rows]
+    const int items = __builtin_amdgcn_readfirstlane(head.x);
+    t = __builtin_amdgcn_readfirstlane(item[0]);
+    c = __builtin_amdgcn_readfirstlane(item[1]);
+    p = __builtin_amdgcn_readfirstlane(item[2]);
+    seq = __builtin_amdgcn_readfirstlane(item[3]);
+    if (int(blockIdx.x) >= items) return;  // past the plan's last item
+    if (__builtin_amdgcn_readfirstlane(head.y) != chunk_tokens ||
+        __builtin_amdgcn_readfirstlane(head.z) != num_chunks ||
+        __builtin_amdgcn_readfirstlane(head.w) != T || t < 0 || t >= T || c < 0 ||
+        c >= num_chunks || p < c * chunk_tokens)
+      return;  // a list built for another launch, or an item outside this one: nothing written
+  } else if (!locate_chunk(blockIdx.x, T, row_pos, row_seq, num_chunks, chunk_tokens, lane, t, c,
+                           p, seq)) {
     return;  // past the batch's last chunk
+  }
   const int s0 = c * chunk_tokens;
   const int n = min(s0 + chunk_tokens, p + 1) - s0;  // positions of this chunk
   // The row has one chunk (its context fits one, or the caller sized one):
@@ -625,7 +649,8 @@ decode_partial_mfma_f32(float* __restrict__ out, float* __restrict__ part_o,
   // the 16-bit kernel.
   const int pi0 = s0 / IE_HIP_PAGE_SIZE;
   const int32_t* row_tab = tables + size_t(seq) * max_pages;
-  const int pid_lane = (16 * lane < n && pi0 + lane < max_pages) ? row_tab[pi0 + lane] : -1;
+  const int pid_lane = plan ? (16 * lane < n ? pid_plan : -1)
+                            : (16 * lane < n && pi0 + lane < max_pages) ? row_tab[pi0 + lane] : -1;
   auto page_id = [&](const int pw) -> int {
     return pw < 64 ? __builtin_amdgcn_readlane(pid_lane, pw) : -1;
   };
@@ -860,7 +885,7 @@ bool decode_mfma_f32_supported(int kv_dtype, int n_heads, int n_kv_heads, int he
 int decode_mfma_f32(float* out, const float* q, const void* k_pool, const void* v_pool, int T,
                     const int32_t* row_pos, const int32_t* row_seq, const ie_kv_layout& kv,
                     int num_chunks, int chunk_tokens, void* workspace, int n_heads,
-                    int n_kv_heads, hipStream_t stream) {
+                    int n_kv_heads, hipStream_t stream, const int32_t* plan) {
   const Workspace ws = carve_workspace(workspace, T, n_heads, 64, num_chunks);
   const int64_t slots = int64_t(T) * num_chunks;  // upper bound on the non-empty chunks
   if (slots * n_heads * 64 * 4 > 0x7fffffff)
@@ -872,7 +897,7 @@ int decode_mfma_f32(float* out, const float* q, const void* k_pool, const void* 
                      2 * kPageF32, stream, out, ws.part_o, ws.part_ml, q,
                      static_cast<const float*>(k_pool), static_cast<const float*>(v_pool), row_pos,
                      row_seq, kv.tables, T, kv.max_pages, kv.num_pages, n_heads,
-                     n_heads / n_kv_heads, num_chunks, chunk_tokens);
+                     n_heads / n_kv_heads, num_chunks, chunk_tokens, plan);
   if (int rc = check_launch("attention_mfma_f32")) return rc;
   return decode_merge(out, ws, row_pos, T, n_heads, num_chunks, chunk_tokens, stream);
 }

@@ -150,10 +150,9 @@ struct Harness {
     std::fflush(stdout);
     op();
     const ie::hip::StepInfo& si = eng->last_step();
-    // Flash-decoding steps of a 16-bit cache that fit one launch read the work
-    // list the engine builds on the host; prompts and f32 caches do not.
-    const bool want_planned = !si.prompt && eng->kv_dtype() != IE_KV_F32 &&
-                              T <= std::max(eng->max_batch(), 16);
+    // Flash-decoding steps that fit one launch read the work list the engine
+    // builds on the host (every KV type); prompts do not.
+    const bool want_planned = !si.prompt && T <= std::max(eng->max_batch(), 16);
     char path[200];
     std::snprintf(path, sizeof(path), "%s: path graph=%d prompt=%d fused=%d planned=%d chunk=%d x %d",
                   name.c_str(), si.graph, si.prompt, si.fused, si.planned, si.chunk_tokens,

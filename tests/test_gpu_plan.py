@@ -202,15 +202,15 @@ def test_config4_fused_planned_full_size(ie, O, dev):
     assert np.array_equal(got.view(np.uint32), from_dev(tout).view(np.uint32))
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_mismatched_plan_writes_nothing(ie, O, dev, fused):
+@pytest.mark.parametrize("fused,kv", [(False, "f16"), (True, "f16"), (False, "f32")])
+def test_mismatched_plan_writes_nothing(ie, O, dev, fused, kv):
     """A plan built for another launch -- another chunk size, or another row count --
     passes the host's capacity check but would address other slots: the kernel
     compares the plan's header with its own arguments and writes nothing, neither
     partials, nor a single-chunk row's output, nor (fused) the appended rows. The
     merge kernel still runs over the untouched workspace, inside its bounds; the
     guard words past `out` and the workspace stay as they were."""
-    kvt = KVS["f16"]
+    kvt = KVS[kv]
     rng = np.random.default_rng(1500 + fused)
     lens = np.array([100, 700, 1500])
     T = len(lens)
