@@ -263,10 +263,10 @@ int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, con
  * is only read and rotated in registers as the prefill kernel loads it (the
  * same arithmetic, so pages and `out` are bit-identical to the two calls; q in
  * memory stays unrotated, and the append skips q's 2 x 3.5 KB per row). Rows
- * as for attention_prefill (consecutive positions of one sequence); the matrix-
- * core prefill kernels only (f32, f16, bf16 caches; head_dim 64, at most 8
- * query heads per KV head; not under IE_HIP_IMPL_VALU), else EINVAL: use the two
- * calls. The table must be 16-byte aligned device memory. */
+ * as for attention_prefill (consecutive positions of one sequence); 16-bit
+ * caches on the matrix-core prefill kernel only (f16, bf16; head_dim 64, at most
+ * 8 query heads per KV head; not under IE_HIP_IMPL_VALU), else EINVAL: use the
+ * two calls. The table must be 16-byte aligned device memory. */
 int ie_hip_rope_cache_attention_prefill_supported(int kv_dtype, int n_heads, int n_kv_heads,
                                                    int head_dim);
 int ie_hip_rope_cache_attention_prefill(float* out, const float* q, const float* k, const float* v,

@@ -92,7 +92,8 @@ struct StepInfo {
   bool graph = false;   // replayed a decode graph
   bool prompt = false;  // prefill attention (rows: consecutive positions of one sequence)
   bool fused = false;   // decode: RoPE + append + attention in one launch per layer;
-                        // prompt: q rotated inside the prefill kernel (append of K/V only)
+                        // prompt: q rotated inside the prefill kernel (append of K/V
+                        // only; 16-bit caches)
   bool planned = false; // flash-decoding read a host-built work list (ie_hip_attention_plan)
   int chunk_tokens = 0, chunks = 0;  // flash-decoding partition (0 for a prompt)
 };

@@ -228,7 +228,7 @@ int ie_hip_attention_prefill(float* out, const float* q, const void* k_pool, con
 
 int ie_hip_rope_cache_attention_prefill_supported(int kv_dtype, int n_heads, int n_kv_heads,
                                                    int head_dim) {
-  return attention_impl() != IE_HIP_IMPL_VALU &&
+  return attention_impl() != IE_HIP_IMPL_VALU && kv_dtype != IE_KV_F32 &&
          prefill_mfma_supported(kv_dtype, n_heads, n_kv_heads, head_dim);
 }
 
@@ -241,9 +241,9 @@ int ie_hip_rope_cache_attention_prefill(float* out, const float* q, const float*
   if (int rc = check_layout(kv, "rope_cache_attention_prefill")) return rc;
   if (!ie_hip_rope_cache_attention_prefill_supported(kv.kv_dtype, n_heads, n_kv_heads, head_dim))
     return fail(IE_HIP_EINVAL,
-                "rope_cache_attention_prefill: needs the matrix-core prefill kernels (head_dim 64, "
-                "at most 8 query heads per KV head, not IE_HIP_IMPL_VALU); use rope_and_cache + "
-                "attention_prefill");
+                "rope_cache_attention_prefill: needs a 16-bit cache and the matrix-core prefill "
+                "kernel (head_dim 64, at most 8 query heads per KV head, not IE_HIP_IMPL_VALU); "
+                "use rope_and_cache + attention_prefill");
   if (T < 0) return fail(IE_HIP_EINVAL, "rope_cache_attention_prefill: negative row count");
   if (T == 0) return IE_HIP_OK;
   if (!out || !q || !k || !v || !k_pool || !v_pool || !rope_table || !row_pos || !row_seq)

@@ -710,8 +710,7 @@ prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
                         const float* __restrict__ k_pool, const float* __restrict__ v_pool, int T,
                         const int32_t* __restrict__ row_pos, const int32_t* __restrict__ row_seq,
                         const int32_t* __restrict__ tables, int max_pages, int num_pages,
-                        int n_heads, int n_kv_heads, int n_blocks,
-                        const float* __restrict__ rope, int rope_positions) {
+                        int n_heads, int n_kv_heads, int n_blocks) {
   // A tile's 32 loads of 1 KB (16 K, 16 V), spread evenly over kDmaWaves waves.
   constexpr int kDmaWaves = kWaves >= 4 ? 4 : kWaves >= 2 ? 2 : 1;
   constexpr int kPerWave = 32 / kDmaWaves;
@@ -792,42 +791,17 @@ prefill_mfma_f32_kernel(float* __restrict__ out, const float* __restrict__ q,
     // Row r's query, times log2(e)/8, at dims 16g .. 16g+15 (B of the score steps).
     float qb[16];
     {
-      const float* qrow = q + (size_t(row_ok ? t : t0) * n_heads + h0) * 64;
+      const float4* src = reinterpret_cast<const float4*>(
+          q + (size_t(row_ok ? t : t0) * n_heads + h0) * 64 + 16 * g);
       const float qs = row_ok ? 0.125f * kLog2e : 0.0f;
-      float x[16];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float4 v = reinterpret_cast<const float4*>(qrow + 16 * g)[i];
-        x[4 * i + 0] = v.x;
-        x[4 * i + 1] = v.y;
-        x[4 * i + 2] = v.z;
-        x[4 * i + 3] = v.w;
+        const float4 x = src[i];
+        qb[4 * i + 0] = x.x * qs;
+        qb[4 * i + 1] = x.y * qs;
+        qb[4 * i + 2] = x.z * qs;
+        qb[4 * i + 3] = x.w * qs;
       }
-      // With a RoPE table, q arrives unrotated and is rotated here as
-      // ie_hip_rope_and_cache would have (the same fmaf, the same float32
-      // values). Dim d = 16g + j pairs with d + 32 (g < 2, this lane holds x0)
-      // or d - 32 (g >= 2, x1): the partner's 16 dims are read as well.
-      if (rope && row_ok && rp >= 0 && rp < rope_positions) {
-        const int i0 = 16 * (g & 1);  // rotation index of dim 16g
-        const float* trow = rope + size_t(rp) * 64 + i0;
-        const float* prow = qrow + 16 * (g ^ 2);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float4 pv = reinterpret_cast<const float4*>(prow)[i];
-          const float4 c4 = reinterpret_cast<const float4*>(trow)[i];
-          const float4 s4 = reinterpret_cast<const float4*>(trow + 32)[i];
-          const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
-          const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float own = x[4 * i + e], other = pp[e];
-            x[4 * i + e] = g < 2 ? __builtin_fmaf(own, cc[e], -(other * ss[e]))  // x0*c - x1*s
-                                 : __builtin_fmaf(own, cc[e], other * ss[e]);    // x1*c + x0*s
-          }
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) qb[i] = x[i] * qs;
     }
     float m = -INFINITY, l = 0.0f;  // running max (base 2), this lane's part of the sum
     f32x4 o[4];                      // o[mt][t]: row r, dim 16g + 4t + mt
@@ -965,7 +939,7 @@ template <int W>
 int launch_prefill_f32(const dim3 grid, float* out, const float* q, const float* kp,
                        const float* vp, int T, const int32_t* row_pos, const int32_t* row_seq,
                        const ie_kv_layout& kv, int n_heads, int n_kv_heads, int n_blocks,
-                       const PrefillRope& rope, hipStream_t stream) {
+                       hipStream_t stream) {
   constexpr int lds = kRingF32 * kBufF32 + 16 * kSegTiles;  // 96 KB ring + the segment's page ids
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(prefill_mfma_f32_kernel<W>),
@@ -973,7 +947,7 @@ int launch_prefill_f32(const dim3 grid, float* out, const float* q, const float*
   if (int rc = check_hip(attr, "hipFuncSetAttribute(attention_prefill_mfma_f32)")) return rc;
   hipLaunchKernelGGL((prefill_mfma_f32_kernel<W>), grid, dim3(64 * W), lds, stream, out, q, kp,
                      vp, T, row_pos, row_seq, kv.tables, kv.max_pages, kv.num_pages, n_heads,
-                     n_kv_heads, n_blocks, rope.table, rope.positions);
+                     n_kv_heads, n_blocks);
   return check_launch("attention_prefill_mfma_f32");
 }
 
@@ -995,6 +969,11 @@ int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const vo
        reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) & 15)
     return fail(IE_HIP_EINVAL, "attention_prefill: q, out and the pools must be 16-byte aligned");
   if (kv.kv_dtype == IE_KV_F32) {
+    // The f32 kernel takes q already rotated (its lanes hold 16 consecutive dims,
+    // not the rotation pairs; reading the partner dims and the table per lane
+    // cost more than the append's q traffic saves).
+    if (rope.table)
+      return fail(IE_HIP_EINVAL, "attention_prefill: f32 caches take q rotated by rope_and_cache");
     const int group = n_heads / n_kv_heads;
     const int n_blocks = (T + kRows - 1) / kRows;
     const dim3 grid((n_blocks + 1) / 2, n_kv_heads);
@@ -1004,7 +983,7 @@ int prefill_mfma_launch(float* out, const float* q, const void* k_pool, const vo
 #define IE_PF32_CASE(W)                                                                      \
   case W:                                                                                    \
     return launch_prefill_f32<W>(grid, out, q, kf, vf, T, row_pos, row_seq, kv, n_heads,     \
-                                 n_kv_heads, n_blocks, rope, stream);
+                                 n_kv_heads, n_blocks, stream);
       IE_PF32_CASE(1)
       IE_PF32_CASE(2)
       IE_PF32_CASE(3)

@@ -270,21 +270,21 @@ int main(int argc, char** argv) {
     const bool f16 = kv != IE_KV_F32;
     // One-row prefill replays the batch-1 decode graph (first token).
     h.prefill(s0, 1, 1, 0, f16, "first token (seq 0, position 0)");
-    h.prefill(s0, 62, 0, 1, 1, "prompt continuing at 1 (62 rows)");
+    h.prefill(s0, 62, 0, 1, f16, "prompt continuing at 1 (62 rows)");
     h.decode({s0}, "decode seq 0 at position 63 (chunk edge 63)");
     h.decode({s0}, "decode seq 0 at position 64 (chunk edge 64)");
-    h.prefill(s1, 17, 0, 1, 1, "prompt of 17 rows (seq 1)");
-    h.prefill(s2, 500, 0, 1, 1, "prompt of 500 rows (seq 2)");
-    h.prefill(s2, 40, 0, 1, 1, "prompt continuing at 500 (40 rows)");
+    h.prefill(s1, 17, 0, 1, f16, "prompt of 17 rows (seq 1)");
+    h.prefill(s2, 500, 0, 1, f16, "prompt of 500 rows (seq 2)");
+    h.prefill(s2, 40, 0, 1, f16, "prompt continuing at 500 (40 rows)");
     const int s3 = eng.open_sequence();
-    h.prefill(s3, 1000, 0, 1, 1, "prompt of 1000 rows (seq 3)");
+    h.prefill(s3, 1000, 0, 1, f16, "prompt of 1000 rows (seq 3)");
     h.decode({s0, s1, s2, s3}, "batch of 4 decodes (graph recorded)");
     h.decode({s0, s1, s2, s3}, "batch of 4 decodes (graph replayed)");
     const int graphs = eng.decode_graphs();
     h.decode({s3, s0, s2, s1}, "batch of 4 decodes, rows reordered");
     result(eng.decode_graphs() == graphs, "batch size 4 replays its graph");
     const int s4 = eng.open_sequence();
-    h.prefill(s4, 255, 0, 1, 1, "prompt of 255 rows (seq 4)");
+    h.prefill(s4, 255, 0, 1, f16, "prompt of 255 rows (seq 4)");
     h.decode({s0, s1, s2, s3, s4}, "batch of 5 decodes (seq 4 at position 255)");
     h.decode({s0, s1, s2, s3, s4}, "batch of 5 decodes (seq 4 at position 256)");
 
@@ -314,7 +314,7 @@ int main(int argc, char** argv) {
            "close_sequence: pages returned");
     const int s6 = eng.open_sequence();
     result(s6 == s1, "open_sequence: reuses the lowest closed slot");
-    h.prefill(s6, 3000, 0, 1, 1, "prompt of 3000 rows on reused pages (seq 1)");
+    h.prefill(s6, 3000, 0, 1, f16, "prompt of 3000 rows on reused pages (seq 1)");
     std::vector<int32_t> p6(eng.max_pages_per_seq());
     eng.sequence_pages(s6, p6.data(), int(p6.size()));
     result(p6[0] == p2[n2 - 1], "reused pages come LIFO (last freed first)");

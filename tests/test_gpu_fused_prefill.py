@@ -3,9 +3,10 @@ prefill attention with q rotated inside the prefill kernel) on the GPU.
 
 The contract: pages and `out` bit-identical to ie_hip_rope_and_cache (q rotated in
 place) followed by ie_hip_attention_prefill on the same inputs (run here on copies), q
-left unmodified, and the oracle's append + attention within the tolerances (f32 cache:
-1e-5 relative; f16/bf16: 2e-3 absolute). Cases: the reference self-test's prompt
-lengths (src/cuda/cuda_runner.cu:920-934), a continuation, a prompt starting mid-tile,
+left unmodified, and the oracle's append + attention within the 16-bit caches'
+tolerance (2e-3 absolute); f32 caches are refused (the caller uses the two calls).
+Cases: the reference self-test's prompt lengths (src/cuda/cuda_runner.cu:920-934), a
+continuation, a prompt starting mid-tile,
 rows whose positions lie past the RoPE table (not appended, queries unrotated, as
 rope_and_cache skips them), a page outside the pool (not written, its keys masked), and
 BASELINE config 5's 4,000-token prompt into a churned pool.
@@ -20,7 +21,7 @@ from helpers import HD, KVD, NH, NKV, QD, THETA, from_dev, kv_pool, make_tables,
 from test_gpu_decode import check
 
 pytestmark = pytest.mark.gpu
-KVS = {"f32": 0, "f16": 1, "bf16": 2}
+KVS = {"f16": 1, "bf16": 2}
 
 
 def run_both(ie, dev, kvt, q, k, v, kp, vp, row_pos, row_seq, tables, max_pages,
@@ -144,10 +145,11 @@ def test_config5_prompt_into_churned_pool(ie, O, dev, kv):
 
 
 def test_unsupported_fails_loudly(ie, dev):
-    """Under the VALU kernels (or at shapes the matrix-core prefill does not take) the
-    call is refused with EINVAL: the caller uses the two calls."""
+    """f32 caches, the VALU kernels and shapes the matrix-core prefill does not take are
+    refused with EINVAL: the caller uses the two calls."""
     assert ie.rope_cache_attention_prefill_supported(ie.KV_F16, NH, NKV, HD)
-    assert ie.rope_cache_attention_prefill_supported(ie.KV_F32, NH, NKV, HD)
+    assert ie.rope_cache_attention_prefill_supported(ie.KV_BF16, NH, NKV, HD)
+    assert not ie.rope_cache_attention_prefill_supported(ie.KV_F32, NH, NKV, HD)
     assert not ie.rope_cache_attention_prefill_supported(ie.KV_F16, NH, NKV, 128)
     prev = ie.set_attention_impl(ie.IMPL_VALU)
     try:
@@ -167,3 +169,9 @@ def test_unsupported_fails_loudly(ie, dev):
                                             to_dev(tables, dev), max_pages, NH, NKV, HD)
     finally:
         ie.set_attention_impl(prev)
+    kp32 = torch.zeros((num_pages * 16, KVD), device=dev)
+    vp32 = torch.zeros_like(kp32)
+    with pytest.raises(ie.IeHipError, match="rope_cache_attention_prefill"):
+        ie.rope_cache_attention_prefill(out, q, kv_rows, kv_rows, kp32, vp32, table, pos, seq,
+                                        to_dev(tables, dev), max_pages, NH, NKV, HD)
+    assert int(kp32.count_nonzero()) == 0
