@@ -6,10 +6,10 @@ place) followed by ie_hip_attention_prefill on the same inputs (run here on copi
 left unmodified, and the oracle's append + attention within the 16-bit caches'
 tolerance (2e-3 absolute); f32 caches are refused (the caller uses the two calls).
 Cases: the reference self-test's prompt lengths (src/cuda/cuda_runner.cu:920-934), a
-continuation, a prompt starting mid-tile,
-rows whose positions lie past the RoPE table (not appended, queries unrotated, as
-rope_and_cache skips them), a page outside the pool (not written, its keys masked), and
-BASELINE config 5's 4,000-token prompt into a churned pool.
+continuation, a prompt starting mid-tile, a prompt whose keys run past 32,768 (page ids
+staged in two segments), rows whose positions lie past the RoPE table (not appended,
+queries unrotated, as rope_and_cache skips them), a page outside the pool (not written,
+its keys masked), and BASELINE config 5's 4,000-token prompt into a churned pool.
 """
 from __future__ import annotations
 
@@ -61,6 +61,7 @@ PROMPTS = [
     ([540], 0, 500, 40),          # a prompt continuing at 500
     ([100, 300], 1, 0, 300),     # the 2nd of 2 sequences
     ([129], 0, 63, 66),          # starts mid-tile, crosses tile edges
+    ([32830], 0, 32750, 80),     # keys past 32,768: the page ids are staged in two segments
 ]
 
 
@@ -76,7 +77,8 @@ def test_matches_two_calls_and_oracle(ie, O, dev, kv, case):
     row_seq = np.full(T, seq, np.int32)
     q, k, v = normal(rng, (T, QD)), normal(rng, (T, KVD)), normal(rng, (T, KVD))
     (fout, fkp, fvp, fq), (tout, tkp, tvp, tq) = run_both(ie, dev, kvt, q, k, v, kp, vp, row_pos,
-                                                          row_seq, tables, max_pages, 2048)
+                                                          row_seq, tables, max_pages,
+                                                          max(2048, start + T))
     assert same_bits(fq, q), "q was modified"
     assert same_bits(fkp, tkp) and same_bits(fvp, tvp), "pages differ from the two calls"
     assert same_bits(fout, tout), "out differs from the two calls"

@@ -2,7 +2,8 @@
 
 Same tolerances as decode (f32: rel 1e-5; f16/bf16: 2e-3 abs). Cases: the
 reference self-test's prompts (src/cuda/cuda_runner.cu:920-934: 1, 17, 300,
-1000 rows; a prompt continuing at 500; the 2nd of 2 sequences) and the
+1000 rows; a prompt continuing at 500; the 2nd of 2 sequences), a prompt whose
+keys run past 32,768 (the kernels stage page ids 512 tiles at a time), and the
 4,000-token prefill of BASELINE config 5, appended into fresh pages of a
 churned pool with the fused RoPE+append kernel first (all 4,000 rows checked
 against the oracle). Decode and prefill kernels must agree on the same rows. The
@@ -47,6 +48,7 @@ PROMPTS = [
     ([540], 0, 500, 40),          # a prompt continuing at 500
     ([100, 300], 1, 0, 300),     # the 2nd of 2 sequences
     ([129], 0, 63, 66),          # starts mid-tile, crosses tile edges
+    ([32830], 0, 32750, 80),     # keys past 32,768: the page ids are staged in two segments
 ]
 
 
