@@ -34,7 +34,7 @@ The default line also carries:
                        physical core count and the threads used; its GB/s counts the
                        CPU's own fp32-cache bytes.
 
-Other configs print the same JSON shape for the tables in DESIGN.md:
+Other configs print the same JSON shape:
   --config 1  the reference's own CPU case (one layer, 512 positions, fp32), GPU and CPU
   --config 2  RoPE + paged append, 64 rows (+ --sweep: rows per launch up to 131,072)
   --config 4  long-context decode, 24 layers, batch 1, 32k context, bf16
@@ -70,7 +70,9 @@ def log(msg: str) -> None:
 
 
 def decode_bytes(lens, kv_bytes: int) -> int:
-    """Algorithmic HBM bytes of one decode-attention launch."""
+    """Algorithmic HBM bytes of one decode-attention launch: per row of context L, the K
+    and V rows of its L positions, its query read and its output written (f32), one page
+    id per page, and its position and sequence."""
     return int(sum(2 * KVD * kv_bytes * L + 2 * QD * 4 + 4 * math.ceil(L / PAGE) + 8 for L in lens))
 
 
