@@ -554,13 +554,18 @@ int ie_hip_attention_chunk_tokens(int T, int max_context, int kv_dtype) {
   if (kv_dtype == IE_KV_F16 || kv_dtype == IE_KV_BF16) {
     // Matrix-core kernel (measured on MI355X): 192-position chunks where rows x
     // chunks at full context still reach 4 workgroups per compute unit (64 rows
-    // of 4,096: 18.5 us per call against 19.5 at 256, 21.0 at 128, 25.1 at 512),
-    // else 128 (one row of 32,768: 11.9 us per layer against 14.1 at 256; 48
-    // rows of 2,049: the decode part 14.6 against 16.4 us at 192). Where the
-    // grid gives two workgroups per compute unit one wave streams each chunk; on
-    // smaller grids each of a chunk's page pairs gets its own wave (same
-    // result), so all are in flight at once.
-    return rows * ie_hip_attention_chunks(ctx, 192) >= 4 * int64_t(cus) ? 192 : 128;
+    // of 4,096: 18.5 us per call against 19.5 at 256, 21.0 at 128, 25.1 at 512);
+    // 64 where even 64-position chunks give at most two workgroups per compute
+    // unit (one row of 32,768: 10.2 us per call against 10.5 at 128, the fused
+    // decode layer 11.1 against 11.9; one row of 8,192: 7.9 against 9.4; 4 rows
+    // of 4,096: 8.5 against 9.7); else 128 (2 rows of 32,768, 16 of 4,096: 13.1
+    // and 12.7 us against 14.5 and 13.3 at 64; 48 rows of 2,049: 16.0 against
+    // 18.6 at 64 and 16.0 at 192). Where the grid gives two workgroups per
+    // compute unit one wave streams each chunk; on smaller grids each of a
+    // chunk's page pairs gets its own wave (same result), so all are in flight
+    // at once.
+    if (rows * ie_hip_attention_chunks(ctx, 192) >= 4 * int64_t(cus)) return 192;
+    return rows * ie_hip_attention_chunks(ctx, 64) <= 2 * int64_t(cus) ? 64 : 128;
   }
   // float32 (matrix-core kernel, one page in flight per wave; measured on
   // MI355X): 192 positions where that gives 4 workgroups per compute unit (64

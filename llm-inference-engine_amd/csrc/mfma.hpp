@@ -204,8 +204,10 @@ __device__ __forceinline__ void round16x2(float x0, float x1, _Float16& h0, _Flo
   h1 = h.y;
 }
 
-// 2^x for the softmax weights: the bare v_exp_f32 (x <= 0 here; results below
-// 2^-126, where it may flush to zero, are far below the weights' tolerance).
+// 2^x for the softmax weights: the bare v_exp_f32 (x is a score minus the row's
+// reference max, at most a few units above 0 where the max is raised lazily;
+// results below 2^-126, where it may flush to zero, are far below the weights'
+// tolerance).
 __device__ __forceinline__ float exp2_weight(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace iehip

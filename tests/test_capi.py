@@ -96,16 +96,19 @@ def test_chunk_helpers(ie):
     assert ie.attention_chunks(4097, 512) == 9
     assert ie.attention_chunks(1, 16) == 1
     # 16-bit caches (matrix-core kernel): 192-token chunks where rows x chunks at full
-    # context reach 4 workgroups per compute unit, else 128 (small grids take one wave
-    # per page pair); float32: 192 where that reaches 4 workgroups per compute unit,
-    # else the largest of 128 and 64 that still gives two, else 32. No GPU here: the helper assumes MI355X's 256
+    # context reach 4 workgroups per compute unit, 64 where rows x 64-token chunks give
+    # at most two, else 128 (small grids take one wave per page pair); float32: 192
+    # where that reaches 4 workgroups per compute unit, else the largest of 128 and 64
+    # that still gives two, else 32. No GPU here: the helper assumes MI355X's 256
     # compute units.
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_F16) == 192   # 64 x 22 = 1,408
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_BF16) == 192
     assert ie.attention_chunk_tokens(64, 2880, ie.KV_F16) == 128   # 64 x 15 < 1,024
     assert ie.attention_chunk_tokens(48, 2049, ie.KV_F16) == 128   # 48 x 11
-    assert ie.attention_chunk_tokens(1, 32768, ie.KV_F16) == 128   # 1 x 171
-    assert ie.attention_chunk_tokens(1, 8192, ie.KV_BF16) == 128
+    assert ie.attention_chunk_tokens(1, 32768, ie.KV_F16) == 64    # 1 x 512 <= 512
+    assert ie.attention_chunk_tokens(1, 8192, ie.KV_BF16) == 64     # 1 x 128
+    assert ie.attention_chunk_tokens(2, 32768, ie.KV_BF16) == 128   # 2 x 512 > 512
+    assert ie.attention_chunk_tokens(16, 4096, ie.KV_F16) == 128    # 16 x 64 > 512
     assert ie.attention_chunk_tokens(8, 131072, ie.KV_BF16) == 192  # 8 x 683
     assert ie.attention_chunk_tokens(64, 4096, ie.KV_F32) == 192
     assert ie.attention_chunk_tokens(48, 2049, ie.KV_F32) == 128   # 48 x 11 < 1,024
