@@ -137,10 +137,11 @@ int ie_hip_rope_and_cache(float* q, const float* k, const float* v, void* k_pool
 /* Chunk size (tokens) for T rows of up to `max_context` tokens with a KV cache
  * of `kv_dtype`, sized for the matrix-core kernel that dtype runs on: for
  * 16-bit caches 192 where T x (chunks at max_context) reaches 4 workgroups per
- * compute unit, else 128 (the kernel splits a chunk one page pair per wave
- * itself when the grid is small, with the same result); for float32 192
- * where that reaches 4 workgroups per compute unit, else the largest of
- * 128/64/32 that still gives two. Results depend on the chunk size, so an engine that wants
+ * compute unit, 64 where T x (64-token chunks) gives at most two, else 128 (the
+ * kernel splits a chunk one page pair per wave itself when the grid is small,
+ * with the same result); for float32 192 where that reaches 4 workgroups per
+ * compute unit, else the largest of 128/64/32 that still gives two. Results
+ * depend on the chunk size, so an engine that wants
  * batch-invariant results fixes it once, from its capacity (max_batch,
  * max_seq_len), as KvEngine does. Replaces the reference's fixed
  * attention_chunks(max_seq_len) sizing (src/cuda/kernels.cu:1387-1391). */
