@@ -91,6 +91,7 @@ prefill_mfma_kernel(float* __restrict__ out, const float* __restrict__ q,
   // hi + lo operands: always for bf16; for f16 under IE_HIP_PREFILL_SPLIT.
   constexpr bool kSplit = kSplitF16 || !std::is_same_v<E, _Float16>;
   constexpr int kRingSteps = kTeams == 1 ? 4 : 3;  // steps of kTeams tiles in LDS
+  static_assert(kSegTiles % kTeams == 0, "a step's tiles never straddle two segments");
   constexpr int kRingBytes = kRingSteps * kTeams * kBufBytes;
   op ones;  // all-ones A operand: row sums of P^T on the matrix cores
 #pragma unroll
